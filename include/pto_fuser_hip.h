@@ -1,0 +1,86 @@
+/* pto_fuser_hip.h — C ABI of the MI355X (gfx950) delta-rule forward library, libptofuser_hip.so.
+ *
+ * This is the drop-in boundary for pto-fuser's chunked delta-rule forward.  The reference
+ * hosts its fused kernels as ctypes-bound `.so` recipes (src/pto_fuser/fused.py:83-162) and its
+ * triangular inverse as an opaque kernel (src/pto_fuser/registry.py:96-127); every entry point
+ * below replaces one of those bindings.  Conventions, all plain C:
+ *   - pointers are device pointers (HBM) unless stated; layouts are row-major and contiguous;
+ *   - `dtype` selects the element type of the q/k/v/w/u operands: PF_DTYPE_F32 or PF_DTYPE_BF16;
+ *     gates (g, beta, decay) are always fp32, outputs are fp32 unless stated;
+ *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream);
+ *     every *_exec only enqueues on that stream: no allocation, no host synchronisation, so it
+ *     is capturable by a HIP graph (the reference's requirement, fused.py:5-9,96-100);
+ *   - every *_exec returns an int status: PF_OK, a negative PF_ERR_* for a contract violation
+ *     detected on the host (nothing is launched), or a positive hipError_t from the launch.
+ *     The reference's execs return void (scan_lib.cpp:90, kkt_fused_lib.cpp:105).
+ *   - *_setup returns an opaque workspace handle owned by the library (NULL on failure) and
+ *     *_teardown frees it (scan_lib.cpp:81-99 discipline: allocate once, launch many).
+ */
+#ifndef PTO_FUSER_HIP_H
+#define PTO_FUSER_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PF_DTYPE_F32 0
+#define PF_DTYPE_BF16 1
+
+#define PF_OK 0
+#define PF_ERR_ARG (-1)       /* shape, dtype or null-pointer contract violated */
+#define PF_ERR_WORKSPACE (-2) /* workspace handle missing or too small for this call */
+#define PF_ERR_ALLOC (-3)     /* setup could not allocate its workspace */
+
+/* Human-readable text for a status code (static storage). */
+const char* pf_status_string(int status);
+/* ABI revision of this library. */
+int pf_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Fused gated delta-rule forward (GDN; DeltaNet when g == NULL).
+ * Replaces the lowered compiled_forward path of examples/attention/gdn.py:75-88: the
+ * kkt_gated_native_v2 FusedNode (fused.py:500-517), the tri_inv_rec_unroll OpaqueNode
+ * (registry.py:107-127), the two WY einsums (_gdn_full.py:199-200), the chunk_h_scan FusedNode
+ * (fused.py:168-182, scan_lib.cpp:81-99) and the qkv_flash_native_v2 FusedNode
+ * (fused.py:353-395, qkv_fused_lib.cpp:148-165), with the host coefficient prep of
+ * prepare_gdn_bindings (_gdn_full.py:103-144) folded in.  Math: gdn_reference
+ * (_gdn_full.py:57-97) plus an initial state h0 and the final state.
+ *   q, k [B,H,T,DK] dtype; v [B,H,T,DV] dtype; beta, g [B,H,T] fp32 (g = per-token log decay,
+ *   summed within each chunk of C tokens by the kernel); h0 [B,H,DK,DV] fp32 or NULL (zero);
+ *   o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV] fp32 or NULL.
+ *   Supported: C = 64, DK = DV = 128, T % C == 0.
+ * ------------------------------------------------------------------------------------------ */
+size_t pf_gdn_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
+void* pf_gdn_setup(int B, int H, int T, int C, int DK, int DV, int dtype);
+int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
+                const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
+                int DV, int dtype, float scale, void* ws, void* stream);
+void pf_gdn_teardown(void* ws);
+
+/* ------------------------------------------------------------------------------------------
+ * Standalone kkt + triangular inverse over M independent chunks.
+ * Replaces the kkt_gated_native FusedNode (fused.py:482-499, kkt_fused_lib.cpp:98-113)
+ * followed by tri_inv_rec_unroll (registry.py:107-127):
+ *   A = strictly_lower(beta_i * safe_exp(G_i - G_j) * k_i.k_j), T = (I + A)^-1
+ *   k [M*C, DK] dtype; g, beta [M*C] fp32 (g_is_cumsum = 1: g already holds G);
+ *   A_out [M,C,C] fp32 or NULL; T_out [M,C,C] fp32.  Supported: C = 64, DK = 128.
+ * ------------------------------------------------------------------------------------------ */
+int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_out, float* T_out,
+                    int M, int C, int DK, int dtype, int g_is_cumsum, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Opaque unit-lower triangular inverse.  Replaces the pto-kernels tri_inv call of
+ * registry.py:124 (`tri_inv(out, A_upper, mi, C, M, 0, cu_seqlens=None, block_dim)`), which
+ * inverts strictly-upper fp16 input: this one takes the strictly-LOWER fp32 A directly.
+ *   A [M,C,C] fp32 (only the strictly-lower part is read); T_out [M,C,C] fp32 = (I + A)^-1.
+ *   Supported: C in {16, 32, 48, 64}.
+ * ------------------------------------------------------------------------------------------ */
+int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PTO_FUSER_HIP_H */

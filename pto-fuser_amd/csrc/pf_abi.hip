@@ -1,0 +1,192 @@
+// extern "C" entry points of libptofuser_hip.so (declared in include/pto_fuser_hip.h).
+//
+// Host-side contract checks happen here, before anything is enqueued; kernels are launched only
+// on the caller's stream, and no exec allocates or synchronises.
+#include <hip/hip_runtime.h>
+
+#include <new>
+
+#include "../../include/pto_fuser_hip.h"
+#include "pf_chunk_local.h"
+#include "pf_scan_output.h"
+
+namespace {
+
+using pf::bf16;
+
+struct GdnWorkspace {
+  void* base = nullptr;
+  size_t bytes = 0;
+};
+
+constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t elem_size(int dtype) { return dtype == PF_DTYPE_BF16 ? 2 : 4; }
+
+bool valid_dtype(int dtype) { return dtype == PF_DTYPE_F32 || dtype == PF_DTYPE_BF16; }
+
+// Byte layout of the fused-forward workspace: [ T (M*C*C E) | P (M*C*C E) | G (M*C fp32) ].
+struct GdnLayout {
+  size_t t_off, p_off, g_off, total;
+  GdnLayout(size_t M, int C, int dtype) {
+    const size_t cc = M * C * C * elem_size(dtype);
+    t_off = 0;
+    p_off = align256(cc);
+    g_off = p_off + align256(cc);
+    total = g_off + align256(M * C * sizeof(float));
+  }
+};
+
+bool gdn_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  return B > 0 && H > 0 && T > 0 && C == 64 && DK == 128 && DV == 128 && T % C == 0 &&
+         valid_dtype(dtype);
+}
+
+int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PF_OK : static_cast<int>(e);
+}
+
+template <typename E>
+int gdn_launch(const void* q, const void* k, const void* v, const float* beta, const float* g,
+               const float* h0, float* o, float* h_final, int B, int H, int T, float scale,
+               const GdnWorkspace* ws, hipStream_t stream) {
+  constexpr int C = 64, DK = 128, DV = 128, NW = 2;
+  const int BH = B * H, NC = T / C;
+  const size_t M = (size_t)BH * NC;
+  const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
+  char* base = static_cast<char*>(ws->base);
+  void* Tm = base + lay.t_off;
+  void* P = base + lay.p_off;
+  float* G = reinterpret_cast<float*>(base + lay.g_off);
+
+  pf::ChunkLocalArgs a1{};
+  a1.k = k;
+  a1.q = q;
+  a1.beta = beta;
+  a1.g = g;
+  a1.G_out = G;
+  a1.T_out = Tm;
+  a1.P_out = P;
+  a1.A_out = nullptr;
+  a1.M = static_cast<int>(M);
+  a1.epi_mode = 0;
+  a1.g_is_cumsum = 0;
+  pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a1);
+  int st = launch_status();
+  if (st != PF_OK) return st;
+
+  pf::ScanOutArgs a2{};
+  a2.q = q;
+  a2.k = k;
+  a2.v = v;
+  a2.beta = beta;
+  a2.G = G;
+  a2.Tm = Tm;
+  a2.P = P;
+  a2.h0 = h0;
+  a2.o = o;
+  a2.h_final = h_final;
+  a2.BH = BH;
+  a2.NC = NC;
+  a2.scale = scale;
+  const unsigned grid = (unsigned)(BH * (DV / (16 * NW)));
+  pf::scan_output_kernel<E, C, DK, DV, NW><<<dim3(grid), dim3(64 * NW), 0, stream>>>(a2);
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pf_status_string(int status) {
+  switch (status) {
+    case PF_OK: return "ok";
+    case PF_ERR_ARG: return "invalid argument (shape, dtype or pointer contract)";
+    case PF_ERR_WORKSPACE: return "workspace missing or too small for this call";
+    case PF_ERR_ALLOC: return "workspace allocation failed";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+  return "unknown status";
+}
+
+int pf_abi_version(void) { return 1; }
+
+size_t pf_gdn_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return 0;
+  return GdnLayout((size_t)B * H * (T / C), C, dtype).total;
+}
+
+void* pf_gdn_setup(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  const size_t bytes = pf_gdn_workspace_bytes(B, H, T, C, DK, DV, dtype);
+  if (bytes == 0) return nullptr;
+  GdnWorkspace* ws = new (std::nothrow) GdnWorkspace();
+  if (!ws) return nullptr;
+  if (hipMalloc(&ws->base, bytes) != hipSuccess) {
+    delete ws;
+    return nullptr;
+  }
+  ws->bytes = bytes;
+  return ws;
+}
+
+void pf_gdn_teardown(void* ws) {
+  GdnWorkspace* w = static_cast<GdnWorkspace*>(ws);
+  if (!w) return;
+  if (w->base) (void)hipFree(w->base);
+  delete w;
+}
+
+int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
+                const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
+                int DV, int dtype, float scale, void* ws, void* stream) {
+  if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
+  if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
+  const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
+  if (!w || !w->base || w->bytes < pf_gdn_workspace_bytes(B, H, T, C, DK, DV, dtype))
+    return PF_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PF_DTYPE_BF16)
+    return gdn_launch<bf16>(q, k, v, beta, g, h0, o, h_final, B, H, T, scale, w, s);
+  return gdn_launch<float>(q, k, v, beta, g, h0, o, h_final, B, H, T, scale, w, s);
+}
+
+int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_out, float* T_out,
+                    int M, int C, int DK, int dtype, int g_is_cumsum, void* stream) {
+  if (M <= 0 || C != 64 || DK != 128 || !valid_dtype(dtype)) return PF_ERR_ARG;
+  if (!k || !beta || !T_out) return PF_ERR_ARG;
+  pf::ChunkLocalArgs a{};
+  a.k = k;
+  a.q = nullptr;
+  a.beta = beta;
+  a.g = g;
+  a.G_out = nullptr;
+  a.T_out = T_out;
+  a.P_out = nullptr;
+  a.A_out = A_out;
+  a.M = M;
+  a.epi_mode = 0;
+  a.g_is_cumsum = g_is_cumsum ? 1 : 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PF_DTYPE_BF16)
+    pf::chunk_local_kernel<bf16, float, 64, 128, false, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(a);
+  else
+    pf::chunk_local_kernel<float, float, 64, 128, false, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(a);
+  return launch_status();
+}
+
+int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream) {
+  if (M <= 0 || !A || !T_out) return PF_ERR_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (C) {
+    case 16: pf::tri_inv_kernel<16><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
+    case 32: pf::tri_inv_kernel<32><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
+    case 48: pf::tri_inv_kernel<48><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
+    case 64: pf::tri_inv_kernel<64><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
+    default: return PF_ERR_ARG;
+  }
+  return launch_status();
+}
+
+}  // extern "C"

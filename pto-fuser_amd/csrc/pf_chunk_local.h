@@ -1,0 +1,223 @@
+// K1 — the chunk-local stage of the chunked delta-rule forward, one workgroup per chunk.
+//
+// For chunk m (C tokens, rows m*C .. m*C+C-1 of the flattened [B*H*T, dk] token axis):
+//   G     = cumsum_within_chunk(g)                                   (_gdn_full.py:63)
+//   A     = strictly_lower( beta_i * safe_exp(G_i - G_j) * (k_i . k_j) )  (_gdn_full.py:73-75)
+//           [epi_mode 1: exp(min(G_i + log beta_i - G_j, 0)), kkt_fused.h:154-185]
+//   T     = (I + A)^-1                                                 (_gdn_full.py:76-78)
+//   P     = causal_incl_diag( (q_i . k_j) * exp(min(G_i - G_j, 0)) )   (_gdn_full.py:91-95)
+//
+// Mapping on CDNA4: k and q chunk tiles are staged in LDS (row pitch padded by 16 bytes so the
+// MFMA operand reads are bank-conflict free per half wave); the 2*NB(NB+1)/2 lower-triangular
+// 16x16 score blocks are spread over the 4 waves and computed with bf16 (or fp32) MFMA; the
+// gate/mask epilogue runs in VALU on the accumulator registers.  The inverse is fp32:
+//   * the NB diagonal 16x16 blocks are inverted by forward substitution, one lane per column,
+//     all blocks at once (16*NB lanes);
+//   * off-diagonal blocks are filled level by level (block distance L = 1..NB-1) with
+//       T_ij = -T_ii * sum_{k=j}^{i-1} A_ik T_kj
+//     on fp32 MFMA (16x16x4), the product chain kept in registers via the permuted-K layout.
+#pragma once
+
+#include "pf_device.h"
+
+namespace pf {
+
+struct ChunkLocalArgs {
+  const void* k;        // [M*C, DK]  E
+  const void* q;        // [M*C, DK]  E        (needed when P is produced)
+  const float* beta;    // [M*C]      fp32
+  const float* g;       // [M*C]      fp32 per-token log decay; null => 0 (DeltaNet)
+  float* G_out;         // [M*C]      within-chunk cumsum (optional)
+  void* T_out;          // [M, C, C]  TO       (optional)
+  void* P_out;          // [M, C, C]  E        (optional)
+  float* A_out;         // [M, C, C]  fp32     (optional)
+  int M;                // number of chunks
+  int epi_mode;         // 0: beta_i*safe_exp(G_i-G_j)   1: exp(min(G_i+log beta_i-G_j, 0))
+  int g_is_cumsum;      // 1: g already holds within-chunk cumulative sums
+};
+
+// (I + A)^-1 of one strictly-lower C x C block held in LDS (As, fp32, pitch C+4) into Ts (same
+// layout); must be called by all 256 threads of the workgroup.  Diagonal 16x16 blocks by
+// lane-parallel forward substitution, then off-diagonal blocks level by level on fp32 MFMA.
+template <int C>
+__device__ __forceinline__ void block_unit_lower_inverse(const float* As, float* Ts) {
+  constexpr int CP = C + 4;
+  constexpr int NB = C / 16;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
+  if (tid < 16 * NB) {
+    const int r = tid >> 4, cc = tid & 15;
+    const float* Ab = As + (16 * r) * CP + 16 * r;
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) s = fmaf(Ab[i * CP + j], t[j], s);
+      if (i > cc) t[i] = -s;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Ts[(16 * r + i) * CP + 16 * r + cc] = t[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int L = 1; L < NB; ++L) {
+    for (int j = w; j + L < NB; j += 4) {
+      const int i = j + L;
+      floatx4 X = zero4();
+      for (int kk = j; kk < i; ++kk) {
+        const float* arow = As + (16 * i + c) * CP + 16 * kk + 4 * g;
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          X = __builtin_amdgcn_mfma_f32_16x16x4f32(arow[ii], Ts[(16 * kk + 4 * g + ii) * CP + 16 * j + c],
+                                                   X, 0, 0, 0);
+      }
+      floatx4 Y = zero4();
+      const float* trow = Ts + (16 * i + c) * CP + 16 * i + 4 * g;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) Y = __builtin_amdgcn_mfma_f32_16x16x4f32(trow[ii], X[ii], Y, 0, 0, 0);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) Ts[(16 * i + 4 * g + ii) * CP + 16 * j + c] = -Y[ii];
+    }
+    __syncthreads();
+  }
+}
+
+template <typename E, typename TO, int C, int DK, bool DO_P, bool DO_INV>
+__global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
+  static_assert(C % 16 == 0 && C <= 64, "chunk size must be 16, 32, 48 or 64");
+  static_assert(DK % Mfma<E>::KB == 0, "head dim must be a multiple of the MFMA K block");
+  constexpr int PE = 16 / sizeof(E);
+  constexpr int KP = DK + PE;   // LDS row pitch of k / q (elements)
+  constexpr int CP = C + 4;     // LDS row pitch of A / T (floats)
+  constexpr int NB = C / 16;
+  constexpr int NL = NB * (NB + 1) / 2;
+  constexpr int VE = Vec16<E>::N;
+
+  __shared__ __attribute__((aligned(16))) E ks[C * KP];
+  __shared__ __attribute__((aligned(16))) E qs[DO_P ? C * KP : 8];
+  __shared__ __attribute__((aligned(16))) float As[C * CP];
+  __shared__ __attribute__((aligned(16))) float Ts[DO_INV ? C * CP : 4];
+  __shared__ float Gs[C], Bs[C];
+
+  const int m = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
+  const size_t row0 = (size_t)m * C;
+
+  // ---- 1. stage k (and q), gates ------------------------------------------------------------
+  {
+    const uint4* kg = reinterpret_cast<const uint4*>(static_cast<const E*>(a.k) + row0 * DK);
+    for (int i = tid; i < C * (DK / VE); i += 256) {
+      const int r = i / (DK / VE), v = i % (DK / VE);
+      *reinterpret_cast<uint4*>(ks + r * KP + v * VE) = kg[i];
+    }
+    if (DO_P) {
+      const uint4* qg = reinterpret_cast<const uint4*>(static_cast<const E*>(a.q) + row0 * DK);
+      for (int i = tid; i < C * (DK / VE); i += 256) {
+        const int r = i / (DK / VE), v = i % (DK / VE);
+        *reinterpret_cast<uint4*>(qs + r * KP + v * VE) = qg[i];
+      }
+    }
+    if (w == 0) {
+      float x = (a.g != nullptr && lane < C) ? a.g[row0 + lane] : 0.f;
+      if (!a.g_is_cumsum) {
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const float y = __shfl_up(x, off);
+          if (lane >= off) x += y;
+        }
+      }
+      if (lane < C) {
+        Gs[lane] = x;
+        Bs[lane] = a.beta[row0 + lane];
+        if (a.G_out) a.G_out[row0 + lane] = x;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. gated score blocks: kkt (A) and, optionally, qk (P) -------------------------------
+  for (int x = w; x < NL * (DO_P ? 2 : 1); x += 4) {
+    const bool is_qk = x >= NL;
+    int idx = is_qk ? x - NL : x, bi = 0;
+    while (idx > bi) { idx -= bi + 1; ++bi; }
+    const int bj = idx;  // (bi, bj), bi >= bj
+    const E* arow = (is_qk ? qs : ks) + (16 * bi + c) * KP;
+    const E* brow = ks + (16 * bj + c) * KP;
+    floatx4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < DK / Mfma<E>::KB; ++kb) acc = Mfma<E>::rows(acc, arow, brow, kb, g);
+    const int j = 16 * bj + c;
+    const float gj = Gs[j];
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int i = 16 * bi + 4 * g + ii;
+      const float gi = Gs[i];
+      if (!is_qk) {
+        float coef;
+        if (a.epi_mode == 0) coef = Bs[i] * safe_exp(gi - gj);
+        else coef = __expf(fminf(gi + __logf(Bs[i]) - gj, 0.f));
+        As[i * CP + j] = (i > j) ? coef * acc[ii] : 0.f;
+      } else {
+        const float val = (i >= j) ? acc[ii] * __expf(fminf(gi - gj, 0.f)) : 0.f;
+        static_cast<E*>(a.P_out)[(size_t)m * C * C + i * C + j] = from_f32<E>(val);
+      }
+    }
+  }
+  if (DO_P) {  // zero the strictly-upper blocks of P (the scan reads whole 32-wide K blocks)
+    E* P = static_cast<E*>(a.P_out) + (size_t)m * C * C;
+    for (int e = tid; e < C * C; e += 256) {
+      const int i = e / C, j = e % C;
+      if ((j >> 4) > (i >> 4)) P[e] = from_f32<E>(0.f);
+    }
+  }
+  __syncthreads();
+
+  if (a.A_out) {
+    float* Ao = a.A_out + (size_t)m * C * C;
+    for (int e = tid; e < C * C; e += 256) {
+      const int i = e / C, j = e % C;
+      Ao[e] = (j < i) ? As[i * CP + j] : 0.f;
+    }
+  }
+
+  if (DO_INV) {
+    block_unit_lower_inverse<C>(As, Ts);
+
+    // ---- 4. write T (lower unit-triangular, zeros above) -----------------------------------
+    TO* To = static_cast<TO*>(a.T_out) + (size_t)m * C * C;
+    for (int e = tid; e < C * C; e += 256) {
+      const int i = e / C, j = e % C;
+      To[e] = from_f32<TO>((j <= i) ? Ts[i * CP + j] : 0.f);
+    }
+  }
+}
+
+}  // namespace pf
+
+namespace pf {
+
+// Standalone opaque inverse: T = (I + A)^-1 for M strictly-lower C x C fp32 blocks (the upper
+// triangle and diagonal of A are ignored, as tril does).  One workgroup per block.
+template <int C>
+__global__ __launch_bounds__(256) void tri_inv_kernel(const float* A, float* T, int M) {
+  constexpr int CP = C + 4;
+  __shared__ __attribute__((aligned(16))) float As[C * CP];
+  __shared__ __attribute__((aligned(16))) float Ts[C * CP];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const float* Ag = A + (size_t)m * C * C;
+  for (int e = tid; e < C * C; e += 256) {
+    const int i = e / C, j = e % C;
+    As[i * CP + j] = (j < i) ? Ag[e] : 0.f;
+  }
+  __syncthreads();
+  block_unit_lower_inverse<C>(As, Ts);
+  float* To = T + (size_t)m * C * C;
+  for (int e = tid; e < C * C; e += 256) {
+    const int i = e / C, j = e % C;
+    To[e] = (j <= i) ? Ts[i * CP + j] : 0.f;
+  }
+}
+
+}  // namespace pf

@@ -1,0 +1,123 @@
+// Device-side building blocks for the gfx950 (CDNA4) delta-rule kernels.
+//
+// Everything here is written for 64-wide wavefronts and the 16x16 MFMA tiles of CDNA4:
+//   bf16:  v_mfma_f32_16x16x32_bf16   (8 bf16 of A and of B per lane, fp32 accumulate)
+//   fp32:  v_mfma_f32_16x16x4_f32     (1 fp32 of A and of B per lane)
+//
+// Lane layout of one 16x16xK MFMA (lane l, group g = l / 16, column c = l % 16):
+//   A operand:  A[row = c][k in the lane's K slice]
+//   B operand:  B[k in the lane's K slice][col = c]
+//   D result :  D[row = 4*g + i][col = c], i = 0..3 (a floatx4 per lane)
+//
+// "Permuted K".  A contraction does not care in which order its K indices are visited, as long
+// as A and B agree.  We choose, per 16-row D block, the K order in which lane group g consumes
+// exactly the four rows 4g..4g+3 that it already holds in its D registers.  Then the output
+// of one MFMA chain (a [16R x 16] D tile) is directly the B operand of the next product that
+// contracts over those R*16 rows — no LDS round trip, no cross-lane shuffle.  The matching A
+// operand reads, for lane (row c, group g), the columns {4g..4g+3} of each 16-column block,
+// i.e. short contiguous runs of the row-major A source.
+//   bf16 (K = 32 per instruction): a K-block of 32 rows = D blocks (2kb, 2kb+1); lane group g
+//        supplies rows {32kb + 4g + 0..3} and {32kb + 16 + 4g + 0..3}.
+//   fp32 (K = 4 per instruction): a K-block of 16 rows = D block kb, consumed by 4 MFMAs; MFMA
+//        i takes row 16kb + 4g + i from lane group g.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pf {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+
+template <typename E> __device__ __forceinline__ E from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+__device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+// exp(x) for x <= 0, 0 for x > 0 (the reference's _safe_exp).
+__device__ __forceinline__ float safe_exp(float x) { return x <= 0.f ? __expf(x) : 0.f; }
+
+// --------------------------------------------------------------------------------------------
+//  MFMA traits.  KB = contraction rows consumed per "K-block" step.
+// --------------------------------------------------------------------------------------------
+template <typename E> struct Mfma;
+
+template <> struct Mfma<bf16> {
+  static constexpr int KB = 32;
+  // acc += A(rows: lane row, K-block kb, permuted) x B(from D blocks d0 = block 2kb, d1 = 2kb+1)
+  __device__ __forceinline__ static floatx4 perm_b(floatx4 acc, const bf16* arow, int kb, int g,
+                                                   const floatx4& d0, const floatx4& d1) {
+    const bf16* p = arow + kb * 32 + 4 * g;
+    bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
+    bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
+    bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    bf16x8 b = {(bf16)d0[0], (bf16)d0[1], (bf16)d0[2], (bf16)d0[3],
+                (bf16)d1[0], (bf16)d1[1], (bf16)d1[2], (bf16)d1[3]};
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+  // acc += A x B^T with both operands read as rows from memory (natural K order).
+  // arow = row (lane c) of A, brow = row (lane c) of B, K-block kb.
+  __device__ __forceinline__ static floatx4 rows(floatx4 acc, const bf16* arow, const bf16* brow,
+                                                 int kb, int g) {
+    bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + kb * 32 + 8 * g);
+    bf16x8 b = *reinterpret_cast<const bf16x8*>(brow + kb * 32 + 8 * g);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<float> {
+  static constexpr int KB = 16;
+  __device__ __forceinline__ static floatx4 perm_b(floatx4 acc, const float* arow, int kb, int g,
+                                                   const floatx4& d0, const floatx4& /*unused*/) {
+    floatx4 a = *reinterpret_cast<const floatx4*>(arow + kb * 16 + 4 * g);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], d0[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], d0[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], d0[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], d0[3], acc, 0, 0, 0);
+    return acc;
+  }
+  __device__ __forceinline__ static floatx4 rows(floatx4 acc, const float* arow, const float* brow,
+                                                 int kb, int g) {
+    floatx4 a = *reinterpret_cast<const floatx4*>(arow + kb * 16 + 4 * g);
+    floatx4 b = *reinterpret_cast<const floatx4*>(brow + kb * 16 + 4 * g);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], acc, 0, 0, 0);
+    return acc;
+  }
+};
+
+// Chain helper: acc += A[this lane's row, 0 : NKB*KB] x D, where D is a register tile of
+// NKB*KB/16 D blocks (16 rows each) consumed in the permuted-K order.  Only the first `kb_end`
+// K-blocks are visited (a triangular A skips its zero blocks); NKB keeps every register index
+// static.
+template <typename E, int NKB>
+__device__ __forceinline__ floatx4 chain(floatx4 acc, const E* arow, const floatx4* d, int kb_end,
+                                         int g) {
+  constexpr int per = Mfma<E>::KB / 16;  // D blocks per K-block (2 for bf16, 1 for fp32)
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < kb_end) acc = Mfma<E>::perm_b(acc, arow, kb, g, d[kb * per], d[kb * per + (per - 1)]);
+  }
+  return acc;
+}
+
+// 16-byte vector type of an element type (8 bf16 or 4 fp32).
+template <typename E> struct Vec16;
+template <> struct Vec16<bf16> { typedef uint4 T; static constexpr int N = 8; };
+template <> struct Vec16<float> { typedef uint4 T; static constexpr int N = 4; };
+
+}  // namespace pf

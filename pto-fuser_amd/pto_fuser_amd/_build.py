@@ -1,0 +1,73 @@
+"""Build libptofuser_hip.so in-tree with hipcc for gfx950.
+
+The library is compiled from ``pto-fuser_amd/csrc/*.hip`` into
+``pto-fuser_amd/pto_fuser_amd/lib/libptofuser_hip.so``; it travels with the source tree, so a
+GPU box loads the file built here.  ``build()`` always recompiles (it is the "does it build"
+check); ``ensure_built()`` compiles only when the library is missing or older than a source.
+"""
+from __future__ import annotations
+
+import glob
+import os
+import shutil
+import subprocess
+from typing import List, Optional
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG_DIR)                       # pto-fuser_amd/
+CSRC = os.path.join(ROOT, "csrc")
+INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_NAME = "libptofuser_hip.so"
+LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+ARCH = os.environ.get("PF_OFFLOAD_ARCH", "gfx950")
+
+# -packed-fp32-ops is disabled: the compiler must not form v_pk_{add,mul,fma}_f32 on its own.
+HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def sources() -> List[str]:
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def headers() -> List[str]:
+    return sorted(glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h")))
+
+
+def build(verbose: bool = False, out: Optional[str] = None) -> str:
+    """Compile every HIP source into the shared library; raises RuntimeError with the compiler
+    output on failure.  Returns the library path."""
+    out = out or LIB_PATH
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + f".tmp{os.getpid()}"
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, *sources(), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"libptofuser_hip build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
+def is_stale(path: str = LIB_PATH) -> bool:
+    if not os.path.exists(path):
+        return True
+    t = os.path.getmtime(path)
+    return any(os.path.getmtime(s) > t for s in sources() + headers())
+
+
+def ensure_built(verbose: bool = False) -> str:
+    """Return the library path, compiling only when no library has been built yet (the GPU box
+    runs the library built in this tree; it never rebuilds a present one)."""
+    if not os.path.exists(LIB_PATH):
+        return build(verbose=verbose)
+    return LIB_PATH

@@ -1,0 +1,117 @@
+"""GPU parity of the fused delta-rule forward and the chunk-local stages against the oracle.
+
+The oracle consumes the dtype-rounded inputs upcast to float64/float32, so the measured error
+is the kernel's arithmetic.  Tolerances (stated per test): fp32 inputs max rel err <= 1e-4;
+bf16 inputs with fp32 accumulation max abs err <= 2e-2 against the fp32 oracle, on o AND the
+final state h.  Config numbers refer to the benchmark configurations (1: DeltaNet fp32 B1 H4
+T512; 2: GDN bf16 B4 H16 T4096; 3: kkt + inverse fp32 over 4096 chunks; 4: GDN bf16 B1 H32
+T32768 with h0).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle.gdn_oracle import (deltanet_reference, gdn_reference, max_abs, max_rel,
+                               tri_inv_reference, within_chunk_cumsum)
+from pto_fuser_amd import gdn_chunk_forward, kkt_inverse, tri_inv
+from pto_fuser_amd.forwards import as_oracle_inputs, make_delta_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+FP32_TOL = 1e-4      # max rel err, fp32 path
+BF16_TOL = 2e-2      # max abs err, bf16 inputs / fp32 accumulation
+
+
+def _run(inp):
+    d = {n: (None if t is None else t.to(DEV)) for n, t in inp.items()}
+    o, h = gdn_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"])
+    torch.cuda.synchronize()
+    return o.cpu().numpy(), h.cpu().numpy()
+
+
+def _oracle(inp, dtype=np.float64):
+    x = as_oracle_inputs(inp)
+    g = x["g"] if x["g"] is not None else np.zeros(x["beta"].shape)
+    return gdn_reference(x["q"], x["k"], x["v"], x["beta"], g, h0=x["h0"], C=64, dtype=dtype)
+
+
+@pytest.mark.parametrize("C", [16, 32, 48, 64])
+def test_tri_inv_matches_oracle(C):
+    announce(f"tri_inv C={C} M=96")
+    rng = np.random.default_rng(C)
+    A = np.tril(rng.standard_normal((96, C, C)) * 0.1, -1).astype(np.float32)
+    A[:, np.arange(C), np.arange(C)] = 5.0                  # diagonal must be ignored
+    A += np.triu(np.ones((C, C), np.float32), 1) * 7.0      # so must the upper triangle
+    got = tri_inv(torch.from_numpy(A).to(DEV)).cpu().numpy()
+    ref = tri_inv_reference(np.tril(A, -1))
+    assert max_rel(got, ref) <= FP32_TOL, max_rel(got, ref)
+    assert np.all(np.triu(got, 1) == 0) and np.all(got[:, np.arange(C), np.arange(C)] == 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kkt_inverse_config3(dtype):
+    """Config 3: 4096 independent 64x64 blocks, A = I + strict-lower(beta k k^T e^{dG}), inverted."""
+    M, C, D = 4096, 64, 128
+    announce(f"kkt_inverse M={M} dtype={dtype}")
+    inp = make_delta_inputs(1, 1, M * C, D, D, kind="gdn", dtype=dtype, seed=3)
+    k = inp["k"].reshape(M * C, D)
+    Tm, A = kkt_inverse(k.to(DEV), inp["g"].reshape(-1).to(DEV), inp["beta"].reshape(-1).to(DEV),
+                        return_A=True)
+    torch.cuda.synchronize()
+    x = as_oracle_inputs(inp)
+    G = within_chunk_cumsum(x["g"], C).reshape(M, C)
+    kk = x["k"].reshape(M, C, D)
+    bt = x["beta"].reshape(M, C)
+    dG = G[:, :, None] - G[:, None, :]
+    A_ref = np.tril(kk @ kk.transpose(0, 2, 1) * np.where(dG <= 0, np.exp(np.minimum(dG, 0)), 0)
+                    * bt[:, :, None], -1)
+    T_ref = tri_inv_reference(A_ref)
+    assert max_rel(A.cpu().numpy(), A_ref) <= FP32_TOL
+    assert max_rel(Tm.cpu().numpy(), T_ref) <= FP32_TOL, max_rel(Tm.cpu().numpy(), T_ref)
+
+
+def test_deltanet_fp32_config1():
+    announce("DeltaNet fp32 B1 H4 T512")
+    inp = make_delta_inputs(1, 4, 512, kind="deltanet", dtype=torch.float32, seed=0)
+    o, h = _run(inp)
+    x = as_oracle_inputs(inp)
+    ref = deltanet_reference(x["q"], x["k"], x["v"], x["beta"], C=64, dtype=np.float64)
+    assert max_rel(o, ref["o"].reshape(o.shape)) <= FP32_TOL
+    assert max_rel(h, ref["final"]) <= FP32_TOL
+
+
+@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 256), (1, 8, 1024)])
+def test_gdn_fp32_with_h0(B, H, T):
+    announce(f"GDN fp32 B{B} H{H} T{T} h0")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.float32, seed=B * 100 + H, h0_std=0.02)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    assert max_rel(o, o_ref) <= FP32_TOL, max_rel(o, o_ref)
+    assert max_rel(h, h_ref) <= FP32_TOL, max_rel(h, h_ref)
+
+
+def test_gdn_bf16_config2():
+    announce("GDN bf16 B4 H16 T4096")
+    inp = make_delta_inputs(4, 16, 4096, kind="gdn", dtype=torch.bfloat16, seed=0)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp, dtype=np.float32)
+    assert max_abs(o, o_ref) <= BF16_TOL, max_abs(o, o_ref)
+    assert max_abs(h, h_ref) <= BF16_TOL, max_abs(h, h_ref)
+
+
+def test_gdn_bf16_config4_long_context():
+    announce("GDN bf16 B1 H32 T32768 h0")
+    inp = make_delta_inputs(1, 32, 32768, kind="gdn", dtype=torch.bfloat16, seed=4, h0_std=0.02)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp, dtype=np.float32)
+    assert max_abs(o, o_ref) <= BF16_TOL, max_abs(o, o_ref)
+    assert max_abs(h, h_ref) <= BF16_TOL, max_abs(h, h_ref)
+
+
+def test_gdn_deterministic():
+    announce("GDN bf16 determinism B2 H8 T1024")
+    inp = make_delta_inputs(2, 8, 1024, kind="gdn", dtype=torch.bfloat16, seed=7)
+    o1, h1 = _run(inp)
+    o2, h2 = _run(inp)
+    assert np.array_equal(o1, o2) and np.array_equal(h1, h2)
