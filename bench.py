@@ -1,0 +1,209 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused GDN chunked forward on one MI355X.
+
+Contract: ``python bench.py --gpus N --steps K --warmup W`` prints ONE JSON line.  A step is
+one full forward of the headline workload (B=4, H=16, T=4096, C=64, dk=dv=128, bf16 inputs,
+fp32 accumulation/state/output) through the C-ABI library: stage 1 (chunk-local gates, kkt,
+(I+A)^-1, gated qk^T) and stage 2 (state scan fused with the output).  Inputs are resident in
+HBM before timing starts; outputs and the workspace are preallocated, so the timed region is
+launches only.  ``value`` is tokens/s = B*T*K / t over exactly K steps bracketed by
+``torch.cuda.synchronize()``.
+
+Besides the required fields the line carries:
+  * ``roofline`` — the dominant kernel's achieved algorithmic HBM bandwidth against the MI355X
+    peak, from HIP events recorded around each launch on the launch stream inside the timed
+    region (per-unit bytes: see ``stage_model``);
+  * ``stages`` — both kernels' average durations, algorithmic bytes and flops, and their
+    HBM / MFMA fractions;
+  * ``cpu_baseline`` — the CPU oracle (a restatement of the reference's per-(b,h,c) loop, fp32
+    numpy, one BLAS thread) timed on this host over the same seeded inputs.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pto-fuser_amd"))
+sys.path.insert(0, ROOT)
+
+WORKLOAD = dict(B=4, H=16, T=4096, C=64, DK=128, DV=128)
+PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
+PEAK_BF16 = 2.5e15         # dense bf16 MFMA, flop/s
+PEAK_FP32 = 157.3e12       # dense fp32 MFMA, flop/s
+METRIC = "GDN chunked-forward tokens/sec at B=4,H=16,T=4096 bf16; % MFMA/HBM roofline"
+
+
+def stage_model(B, H, T, C, DK, DV, esize):
+    """Algorithmic flops and HBM bytes per launch of the two kernels.
+
+    Unit = one (b,h) chunk of C tokens; a launch processes M = B*H*T/C units.
+      stage 1 (chunk-local): reads k, q (2*C*DK*e) + g, beta (2*C*4); writes T, P (2*C*C*e) +
+               G (C*4).  flops: k k^T and q k^T (2 * 2*C*C*DK) + inverse (C^3/3).
+      stage 2 (scan+output): reads q, k, v (2*C*DK*e + C*DV*e), T, P (2*C*C*e), G, beta
+               (2*C*4); writes o (C*DV*4); plus the final state (DK*DV*4) once per chain.
+               flops: k S, q S, k^T v_new (3 * 2*C*DK*DV) + T r, P v_new (2 * 2*C*C*DV).
+    """
+    M = B * H * (T // C)
+    s1_bytes = 2 * C * DK * esize + 2 * C * 4 + 2 * C * C * esize + C * 4
+    s1_flops = 2 * (2 * C * C * DK) + C ** 3 / 3
+    s2_bytes = (2 * C * DK + C * DV) * esize + 2 * C * C * esize + 2 * C * 4 + C * DV * 4
+    s2_flops = 3 * (2 * C * DK * DV) + 2 * (2 * C * C * DV)
+    return {
+        "chunk_local": {"units": M, "bytes_per_unit": s1_bytes, "flops_per_unit": s1_flops,
+                        "bytes": M * s1_bytes, "flops": M * s1_flops},
+        "scan_output": {"units": M, "bytes_per_unit": s2_bytes, "flops_per_unit": s2_flops,
+                        "bytes": M * s2_bytes + B * H * DK * DV * 4, "flops": M * s2_flops},
+    }
+
+
+def cpu_baseline(inputs, runs: int = 3):
+    """Time the CPU oracle (reference loop structure, fp32) on the full workload, one BLAS
+    thread; median of ``runs`` after a one-chain warmup."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle.gdn_oracle import gdn_reference
+
+    x = {n: (None if t is None else t.float().numpy()) for n, t in inputs.items()}
+    B, H, T = x["beta"].shape
+    times = []
+    with threadpool_limits(1):
+        gdn_reference(x["q"][:1, :1], x["k"][:1, :1], x["v"][:1, :1], x["beta"][:1, :1],
+                      x["g"][:1, :1], C=WORKLOAD["C"], dtype=np.float32, loop=True)
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            gdn_reference(x["q"], x["k"], x["v"], x["beta"], x["g"], C=WORKLOAD["C"],
+                          dtype=np.float32, loop=True)
+            times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": B * T / t, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": (f"full workload B{B} H{H} T{T} (all {B * H} chains x {T // WORKLOAD['C']} "
+                       f"chunks), numpy fp32 oracle in the reference's b,h,c loop order, "
+                       f"1 BLAS thread, median of {runs} runs ({', '.join(f'{s:.2f}' for s in times)} s)")}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-runs", type=int, default=3)
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): this "
+              f"build has no multi-GPU path; the forward shards over (b,h) chains with no "
+              f"communication, so per-GPU throughput at N GPUs is the N=1 figure.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from pto_fuser_amd import _hip
+    from pto_fuser_amd.forwards import make_delta_inputs
+    from pto_fuser_amd.ops import gdn_workspace
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, T, C, DK, DV = (WORKLOAD[k] for k in ("B", "H", "T", "C", "DK", "DV"))
+    dtype = torch.bfloat16
+    inputs = make_delta_inputs(B, H, T, DK, DV, kind="gdn", dtype=dtype, seed=0)
+    d = {n: (None if t is None else t.to(dev)) for n, t in inputs.items()}
+    o = torch.empty(B, H, T, DV, device=dev, dtype=torch.float32)
+    hf = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32)
+    ws = gdn_workspace(B, H, T, C, DK, DV, dtype, dev)
+    lib = _hip.load()
+    code = _hip.PF_DTYPE_BF16
+    scale = DK ** -0.5
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    P = {n: _hip.ptr(t) for n, t in d.items()}
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        st = lib.pf_gdn_chunk_local_exec(P["q"], P["k"], P["beta"], P["g"], B, H, T, C, DK, DV,
+                                         code, ws.handle, sh)
+        if st:
+            _hip.check("pf_gdn_chunk_local_exec", st)
+        if ev is not None:
+            ev[1].record(stream)
+        st = lib.pf_gdn_scan_output_exec(P["q"], P["k"], P["v"], P["beta"], None, _hip.ptr(o),
+                                         _hip.ptr(hf), B, H, T, C, DK, DV, code, scale, ws.handle,
+                                         sh)
+        if st:
+            _hip.check("pf_gdn_scan_output_exec", st)
+        if ev is not None:
+            ev[2].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) / args.steps * 1e3
+    k1_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    k2_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in events)
+
+    model = stage_model(B, H, T, C, DK, DV, esize=2)
+    stages = {}
+    for name, ms in (("chunk_local", k1_ms), ("scan_output", k2_ms)):
+        m = model[name]
+        s = ms * 1e-3
+        stages[name] = {
+            "avg_ms": round(ms, 5), "bytes": m["bytes"], "flops": m["flops"],
+            "bytes_per_unit": m["bytes_per_unit"], "flops_per_unit": m["flops_per_unit"],
+            "units": m["units"],
+            "hbm_GBps": round(m["bytes"] / s / 1e9, 1),
+            "hbm_frac": round(m["bytes"] / s / PEAK_HBM, 4),
+            "mfma_TFLOPs": round(m["flops"] / s / 1e12, 2),
+            "mfma_bf16_frac": round(m["flops"] / s / PEAK_BF16, 4),
+        }
+    dom = max(stages, key=lambda n: stages[n]["avg_ms"])
+    ds = stages[dom]
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": ds["hbm_GBps"],
+                "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": ds["hbm_frac"], "traffic": None}
+    total_bytes = sum(model[n]["bytes"] for n in model)
+    total_flops = sum(model[n]["flops"] for n in model)
+
+    line = {
+        "metric": METRIC,
+        "value": round(B * T / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian q/k/v, sigmoid beta, -softplus*0.1 log-decay)",
+        "config": {"workload": "GDN chunked forward B4 H16 T4096 C64 dk128 dv128, bf16 in, "
+                               "fp32 state/accum/o", **WORKLOAD},
+        "roofline": roofline,
+        "stages": stages,
+        "forward": {"bytes": total_bytes, "flops": total_flops,
+                    "hbm_frac": round(total_bytes / (ms_per_step * 1e-3) / PEAK_HBM, 4),
+                    "mfma_bf16_frac": round(total_flops / (ms_per_step * 1e-3) / PEAK_BF16, 4)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(inputs, runs=args.cpu_runs)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -48,51 +48,64 @@ int launch_status() {
 }
 
 template <typename E>
-int gdn_launch(const void* q, const void* k, const void* v, const float* beta, const float* g,
-               const float* h0, float* o, float* h_final, int B, int H, int T, float scale,
-               const GdnWorkspace* ws, hipStream_t stream) {
-  constexpr int C = 64, DK = 128, DV = 128, NW = 2;
-  const int BH = B * H, NC = T / C;
+int chunk_local_launch(const void* q, const void* k, const float* beta, const float* g,
+                       const GdnWorkspace* ws, size_t M, hipStream_t stream) {
+  constexpr int C = 64, DK = 128;
+  const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
+  char* base = static_cast<char*>(ws->base);
+  pf::ChunkLocalArgs a{};
+  a.k = k;
+  a.q = q;
+  a.beta = beta;
+  a.g = g;
+  a.G_out = reinterpret_cast<float*>(base + lay.g_off);
+  a.T_out = base + lay.t_off;
+  a.P_out = base + lay.p_off;
+  a.A_out = nullptr;
+  a.M = static_cast<int>(M);
+  a.epi_mode = 0;
+  a.g_is_cumsum = 0;
+  pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
+  return launch_status();
+}
+
+template <typename E>
+int scan_output_launch(const void* q, const void* k, const void* v, const float* beta,
+                       const float* h0, float* o, float* h_final, int BH, int NC, float scale,
+                       const GdnWorkspace* ws, hipStream_t stream) {
+  constexpr int C = 64, DK = 128, DV = 128, NWC = 2;
   const size_t M = (size_t)BH * NC;
   const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
   char* base = static_cast<char*>(ws->base);
-  void* Tm = base + lay.t_off;
-  void* P = base + lay.p_off;
-  float* G = reinterpret_cast<float*>(base + lay.g_off);
-
-  pf::ChunkLocalArgs a1{};
-  a1.k = k;
-  a1.q = q;
-  a1.beta = beta;
-  a1.g = g;
-  a1.G_out = G;
-  a1.T_out = Tm;
-  a1.P_out = P;
-  a1.A_out = nullptr;
-  a1.M = static_cast<int>(M);
-  a1.epi_mode = 0;
-  a1.g_is_cumsum = 0;
-  pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a1);
-  int st = launch_status();
-  if (st != PF_OK) return st;
-
-  pf::ScanOutArgs a2{};
-  a2.q = q;
-  a2.k = k;
-  a2.v = v;
-  a2.beta = beta;
-  a2.G = G;
-  a2.Tm = Tm;
-  a2.P = P;
-  a2.h0 = h0;
-  a2.o = o;
-  a2.h_final = h_final;
-  a2.BH = BH;
-  a2.NC = NC;
-  a2.scale = scale;
-  const unsigned grid = (unsigned)(BH * (DV / (16 * NW)));
-  pf::scan_output_kernel<E, C, DK, DV, NW><<<dim3(grid), dim3(64 * NW), 0, stream>>>(a2);
+  pf::ScanOutArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.beta = beta;
+  a.G = reinterpret_cast<const float*>(base + lay.g_off);
+  a.Tm = base + lay.t_off;
+  a.P = base + lay.p_off;
+  a.h0 = h0;
+  a.o = o;
+  a.h_final = h_final;
+  a.BH = BH;
+  a.NC = NC;
+  a.scale = scale;
+  const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
+  // Two LDS chunk buffers fit for bf16 operands (2 x 75 KB); fp32 images need one.
+  constexpr int NBUF = std::is_same<E, bf16>::value ? 2 : 1;
+  pf::scan_output_kernel<E, C, DK, DV, NWC, NBUF>
+      <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
   return launch_status();
+}
+
+// Shared host checks of the three GDN entry points.
+int gdn_check(int B, int H, int T, int C, int DK, int DV, int dtype, const void* ws) {
+  if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
+  const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
+  if (!w || !w->base || w->bytes < GdnLayout((size_t)B * H * (T / C), C, dtype).total)
+    return PF_ERR_WORKSPACE;
+  return PF_OK;
 }
 
 }  // namespace
@@ -138,18 +151,43 @@ void pf_gdn_teardown(void* ws) {
   delete w;
 }
 
+int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, const float* g,
+                            int B, int H, int T, int C, int DK, int DV, int dtype, void* ws,
+                            void* stream) {
+  const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
+  if (st != PF_OK) return st;
+  if (!q || !k || !beta) return PF_ERR_ARG;
+  const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
+  const size_t M = (size_t)B * H * (T / C);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PF_DTYPE_BF16) return chunk_local_launch<bf16>(q, k, beta, g, w, M, s);
+  return chunk_local_launch<float>(q, k, beta, g, w, M, s);
+}
+
+int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const float* beta,
+                            const float* h0, float* o, float* h_final, int B, int H, int T, int C,
+                            int DK, int DV, int dtype, float scale, void* ws, void* stream) {
+  const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
+  if (st != PF_OK) return st;
+  if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
+  const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PF_DTYPE_BF16)
+    return scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, scale, w, s);
+  return scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, scale, w, s);
+}
+
 int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
                 const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
                 int DV, int dtype, float scale, void* ws, void* stream) {
-  if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
-  if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
-  const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
-  if (!w || !w->base || w->bytes < pf_gdn_workspace_bytes(B, H, T, C, DK, DV, dtype))
-    return PF_ERR_WORKSPACE;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PF_DTYPE_BF16)
-    return gdn_launch<bf16>(q, k, v, beta, g, h0, o, h_final, B, H, T, scale, w, s);
-  return gdn_launch<float>(q, k, v, beta, g, h0, o, h_final, B, H, T, scale, w, s);
+  if (!q || !k || !v || !beta || !o) {
+    const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
+    return st != PF_OK ? st : PF_ERR_ARG;
+  }
+  const int st = pf_gdn_chunk_local_exec(q, k, beta, g, B, H, T, C, DK, DV, dtype, ws, stream);
+  if (st != PF_OK) return st;
+  return pf_gdn_scan_output_exec(q, k, v, beta, h0, o, h_final, B, H, T, C, DK, DV, dtype, scale,
+                                 ws, stream);
 }
 
 int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_out, float* T_out,

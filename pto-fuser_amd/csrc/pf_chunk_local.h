@@ -94,33 +94,48 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   constexpr int NB = C / 16;
   constexpr int NL = NB * (NB + 1) / 2;
   constexpr int VE = Vec16<E>::N;
+  constexpr int NV = C * (DK / VE);                 // 16-byte vectors per k (or q) chunk tile
+  constexpr int NVT = NV / 256;                     // per thread
+  static_assert(NV % 256 == 0, "k/q chunk tile must divide over 256 threads");
+  constexpr int KQ_BYTES = (DO_P ? 2 : 1) * C * KP * (int)sizeof(E);
+  constexpr int T_BYTES = DO_INV ? C * CP * 4 : 16;
+  // T is written only after the last score read of k/q (a barrier apart), so it reuses their LDS.
+  constexpr int KQT_BYTES = KQ_BYTES > T_BYTES ? KQ_BYTES : T_BYTES;
 
-  __shared__ __attribute__((aligned(16))) E ks[C * KP];
-  __shared__ __attribute__((aligned(16))) E qs[DO_P ? C * KP : 8];
+  __shared__ __attribute__((aligned(16))) char kqt[KQT_BYTES];
   __shared__ __attribute__((aligned(16))) float As[C * CP];
-  __shared__ __attribute__((aligned(16))) float Ts[DO_INV ? C * CP : 4];
   __shared__ float Gs[C], Bs[C];
+  E* ks = reinterpret_cast<E*>(kqt);
+  E* qs = ks + C * KP;
+  float* Ts = reinterpret_cast<float*>(kqt);
 
   const int m = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const size_t row0 = (size_t)m * C;
 
-  // ---- 1. stage k (and q), gates ------------------------------------------------------------
+  // ---- 1. stage k (and q), gates: every load issued before the first LDS store ----------------
   {
     const uint4* kg = reinterpret_cast<const uint4*>(static_cast<const E*>(a.k) + row0 * DK);
-    for (int i = tid; i < C * (DK / VE); i += 256) {
-      const int r = i / (DK / VE), v = i % (DK / VE);
-      *reinterpret_cast<uint4*>(ks + r * KP + v * VE) = kg[i];
+    const uint4* qg = reinterpret_cast<const uint4*>(static_cast<const E*>(a.q) + row0 * DK);
+    uint4 kr[NVT], qr[NVT];
+#pragma unroll
+    for (int i = 0; i < NVT; ++i) {
+      kr[i] = kg[tid + 256 * i];
+      qr[i] = DO_P ? qg[tid + 256 * i] : make_uint4(0u, 0u, 0u, 0u);
     }
-    if (DO_P) {
-      const uint4* qg = reinterpret_cast<const uint4*>(static_cast<const E*>(a.q) + row0 * DK);
-      for (int i = tid; i < C * (DK / VE); i += 256) {
-        const int r = i / (DK / VE), v = i % (DK / VE);
-        *reinterpret_cast<uint4*>(qs + r * KP + v * VE) = qg[i];
-      }
+    float x = 0.f, bv = 0.f;
+    if (tid < C) {
+      x = a.g != nullptr ? a.g[row0 + tid] : 0.f;
+      bv = a.beta[row0 + tid];
+    }
+#pragma unroll
+    for (int i = 0; i < NVT; ++i) {
+      const int u = tid + 256 * i;
+      const int r = u / (DK / VE), v = u % (DK / VE);
+      *reinterpret_cast<uint4*>(ks + r * KP + v * VE) = kr[i];
+      if (DO_P) *reinterpret_cast<uint4*>(qs + r * KP + v * VE) = qr[i];
     }
     if (w == 0) {
-      float x = (a.g != nullptr && lane < C) ? a.g[row0 + lane] : 0.f;
       if (!a.g_is_cumsum) {
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -130,7 +145,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
       }
       if (lane < C) {
         Gs[lane] = x;
-        Bs[lane] = a.beta[row0 + lane];
+        Bs[lane] = bv;
         if (a.G_out) a.G_out[row0 + lane] = x;
       }
     }
@@ -165,11 +180,11 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
       }
     }
   }
-  if (DO_P) {  // zero the strictly-upper blocks of P (the scan reads whole 32-wide K blocks)
-    E* P = static_cast<E*>(a.P_out) + (size_t)m * C * C;
-    for (int e = tid; e < C * C; e += 256) {
-      const int i = e / C, j = e % C;
-      if ((j >> 4) > (i >> 4)) P[e] = from_f32<E>(0.f);
+  if (DO_P) {  // zero the strictly-upper 16x16 blocks of P (the scan reads whole K blocks)
+    uint4* P = reinterpret_cast<uint4*>(static_cast<E*>(a.P_out) + (size_t)m * C * C);
+    for (int u = tid; u < C * C / VE; u += 256) {
+      const int i = u / (C / VE), j0 = (u % (C / VE)) * VE;
+      if ((j0 >> 4) > (i >> 4)) P[u] = make_uint4(0u, 0u, 0u, 0u);
     }
   }
   __syncthreads();
@@ -185,11 +200,13 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   if (DO_INV) {
     block_unit_lower_inverse<C>(As, Ts);
 
-    // ---- 4. write T (lower unit-triangular, zeros above) -----------------------------------
+    // ---- 4. write T (lower unit-triangular, zeros above), four columns per store ----------
     TO* To = static_cast<TO*>(a.T_out) + (size_t)m * C * C;
-    for (int e = tid; e < C * C; e += 256) {
-      const int i = e / C, j = e % C;
-      To[e] = from_f32<TO>((j <= i) ? Ts[i * CP + j] : 0.f);
+    for (int u = tid; u < C * C / 4; u += 256) {
+      const int i = u / (C / 4), j0 = (u % (C / 4)) * 4;
+      const floatx4 t4 = *reinterpret_cast<const floatx4*>(Ts + i * CP + j0);
+      store4(To + i * C + j0, (j0 <= i) ? t4[0] : 0.f, (j0 + 1 <= i) ? t4[1] : 0.f,
+             (j0 + 2 <= i) ? t4[2] : 0.f, (j0 + 3 <= i) ? t4[3] : 0.f);
     }
   }
 }

@@ -50,18 +50,39 @@ __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f};
 __device__ __forceinline__ float safe_exp(float x) { return x <= 0.f ? __expf(x) : 0.f; }
 
 // --------------------------------------------------------------------------------------------
+//  Swizzled LDS tiles.  A tile is row-major with `pitch` elements per row; its 4-element column
+//  groups are XOR-permuted by row bits, group' = group ^ ((row >> RS) & RM), so that the MFMA
+//  operand reads (16 rows x one group) and the transposed staging writes (rows 8 apart) spread
+//  over all banks.  RM = 0 is the plain layout.  With RM = 1 a 16-byte vector (two bf16 groups)
+//  stays in place and only its two 8-byte halves swap.
+// --------------------------------------------------------------------------------------------
+template <int RS, int RM>
+struct Swz {
+  static constexpr int rs = RS, rm = RM;
+  __device__ __forceinline__ static int off(int row, int col, int pitch) {
+    return row * pitch + ((((col >> 2) ^ ((row >> RS) & RM)) << 2) | (col & 3));
+  }
+  // element offset of the 4-element group holding column `col` (col % 4 == 0)
+  __device__ __forceinline__ static int grp(int row, int col, int pitch) {
+    return row * pitch + (((col >> 2) ^ ((row >> RS) & RM)) << 2);
+  }
+};
+
+// --------------------------------------------------------------------------------------------
 //  MFMA traits.  KB = contraction rows consumed per "K-block" step.
 // --------------------------------------------------------------------------------------------
 template <typename E> struct Mfma;
 
 template <> struct Mfma<bf16> {
   static constexpr int KB = 32;
-  // acc += A(rows: lane row, K-block kb, permuted) x B(from D blocks d0 = block 2kb, d1 = 2kb+1)
-  __device__ __forceinline__ static floatx4 perm_b(floatx4 acc, const bf16* arow, int kb, int g,
-                                                   const floatx4& d0, const floatx4& d1) {
-    const bf16* p = arow + kb * 32 + 4 * g;
-    bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
-    bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
+  // acc += A x B, A = row `row` of a swizzled tile (K-block kb, permuted K order), B = the two
+  // D blocks (2kb, 2kb+1) of a register tile.
+  template <class SW>
+  __device__ __forceinline__ static floatx4 perm_b(floatx4 acc, const bf16* tile, int row, int pitch,
+                                                   int kb, int g, const floatx4& d0,
+                                                   const floatx4& d1) {
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(tile + SW::grp(row, kb * 32 + 4 * g, pitch));
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(tile + SW::grp(row, kb * 32 + 16 + 4 * g, pitch));
     bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     bf16x8 b = {(bf16)d0[0], (bf16)d0[1], (bf16)d0[2], (bf16)d0[3],
                 (bf16)d1[0], (bf16)d1[1], (bf16)d1[2], (bf16)d1[3]};
@@ -79,9 +100,11 @@ template <> struct Mfma<bf16> {
 
 template <> struct Mfma<float> {
   static constexpr int KB = 16;
-  __device__ __forceinline__ static floatx4 perm_b(floatx4 acc, const float* arow, int kb, int g,
-                                                   const floatx4& d0, const floatx4& /*unused*/) {
-    floatx4 a = *reinterpret_cast<const floatx4*>(arow + kb * 16 + 4 * g);
+  template <class SW>
+  __device__ __forceinline__ static floatx4 perm_b(floatx4 acc, const float* tile, int row, int pitch,
+                                                   int kb, int g, const floatx4& d0,
+                                                   const floatx4& /*unused*/) {
+    floatx4 a = *reinterpret_cast<const floatx4*>(tile + SW::grp(row, kb * 16 + 4 * g, pitch));
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], d0[0], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], d0[1], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], d0[2], acc, 0, 0, 0);
@@ -100,20 +123,36 @@ template <> struct Mfma<float> {
   }
 };
 
-// Chain helper: acc += A[this lane's row, 0 : NKB*KB] x D, where D is a register tile of
-// NKB*KB/16 D blocks (16 rows each) consumed in the permuted-K order.  Only the first `kb_end`
-// K-blocks are visited (a triangular A skips its zero blocks); NKB keeps every register index
-// static.
-template <typename E, int NKB>
-__device__ __forceinline__ floatx4 chain(floatx4 acc, const E* arow, const floatx4* d, int kb_end,
-                                         int g) {
+// Chain helper: acc += A[row, 0 : NKB*KB] x D, where A is row `row` of a swizzled LDS tile and D
+// is a register tile of NKB*KB/16 D blocks (16 rows each) consumed in the permuted-K order.
+// Only the first `kb_end` K-blocks are visited (a triangular A skips its zero blocks); NKB keeps
+// every register index static.
+template <typename E, int NKB, class SW>
+__device__ __forceinline__ floatx4 chain(floatx4 acc, const E* tile, int row, int pitch,
+                                         const floatx4* d, int kb_end, int g) {
   constexpr int per = Mfma<E>::KB / 16;  // D blocks per K-block (2 for bf16, 1 for fp32)
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < kb_end) acc = Mfma<E>::perm_b(acc, arow, kb, g, d[kb * per], d[kb * per + (per - 1)]);
+    if (kb < kb_end)
+      acc = Mfma<E>::template perm_b<SW>(acc, tile, row, pitch, kb, g, d[kb * per], d[kb * per + (per - 1)]);
   }
   return acc;
 }
+
+// Store four consecutive values as one vector (8 bytes of bf16 or 16 bytes of fp32).
+__device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
+  *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+}
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<floatx4*>(p) = floatx4{a, b, c, d};
+}
+
+// Four consecutive elements as fp32.
+__device__ __forceinline__ floatx4 load4f(const bf16* p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return floatx4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+__device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
 
 // 16-byte vector type of an element type (8 bf16 or 4 fp32).
 template <typename E> struct Vec16;
