@@ -93,6 +93,9 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="after the timed steps, run three plain device copies of MIB MiB: the "
+                         "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -199,6 +202,14 @@ def main(argv=None) -> int:
                     "hbm_frac": round(total_bytes / (ms_per_step * 1e-3) / PEAK_HBM, 4),
                     "mfma_bf16_frac": round(total_flops / (ms_per_step * 1e-3) / PEAK_BF16, 4)},
     }
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["calibration_copy_bytes"] = n * 4
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(inputs, runs=args.cpu_runs)
     print(json.dumps(line), flush=True)

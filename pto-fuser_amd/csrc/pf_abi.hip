@@ -9,6 +9,11 @@
 #include "../../include/pto_fuser_hip.h"
 #include "pf_chunk_local.h"
 #include "pf_scan_output.h"
+#include "pf_scan_output_tr.h"
+
+#ifndef PF_TR_LOADER_WAVES
+#define PF_TR_LOADER_WAVES 4
+#endif
 
 namespace {
 
@@ -92,10 +97,15 @@ int scan_output_launch(const void* q, const void* k, const void* v, const float*
   a.NC = NC;
   a.scale = scale;
   const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
-  // Two LDS chunk buffers fit for bf16 operands (2 x 75 KB); fp32 images need one.
-  constexpr int NBUF = std::is_same<E, bf16>::value ? 2 : 1;
-  pf::scan_output_kernel<E, C, DK, DV, NWC, NBUF>
-      <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
+  if constexpr (std::is_same<E, bf16>::value) {
+    // bf16: row-major staging read back through LDS transpose loads (gfx950)
+    constexpr int NLW = PF_TR_LOADER_WAVES;
+    pf::scan_output_tr_kernel<C, DK, DV, NWC, NLW><<<dim3(grid), dim3(64 * (NWC + NLW)), 0, stream>>>(a);
+  } else {
+    // fp32: transposed tiles staged by the loader; one LDS buffer (the images are 143 KB)
+    pf::scan_output_kernel<E, C, DK, DV, NWC, 1>
+        <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
+  }
   return launch_status();
 }
 

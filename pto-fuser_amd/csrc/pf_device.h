@@ -46,6 +46,19 @@ template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
+// Workgroup barrier that orders LDS traffic only.  __syncthreads() is a workgroup memory fence:
+// it waits for every outstanding global load and store of the wave (vmcnt(0)) before the
+// barrier, which turns register prefetches into synchronous HBM round trips.  Here the wave waits
+// only for its own LDS operations (lgkmcnt(0); vmcnt and expcnt left at their maxima), so loads
+// and stores to global memory stay in flight across the barrier.  Valid because no wave of these
+// kernels reads global data that another wave of the same workgroup writes.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // gfx9 encoding: vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
+}
+
 // exp(x) for x <= 0, 0 for x > 0 (the reference's _safe_exp).
 __device__ __forceinline__ float safe_exp(float x) { return x <= 0.f ? __expf(x) : 0.f; }
 

@@ -132,7 +132,8 @@ __device__ __forceinline__ void put_row16(E* tile, int row, int col, int pitch, 
 }
 
 template <typename E, int C, int DK, int DV, int NWC, int NBUF>
-__global__ __launch_bounds__(64 * (NWC + kLoaderWaves)) void scan_output_kernel(ScanOutArgs a) {
+__global__ __launch_bounds__(64 * (NWC + kLoaderWaves)) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void scan_output_kernel(ScanOutArgs a) {
   constexpr int TW = 16 * NWC;
   using Stage = ChunkStage<E, C, DK, TW>;
   using Regs = ChunkRegs<E, C, DK, TW>;
@@ -337,29 +338,29 @@ __global__ __launch_bounds__(64 * (NWC + kLoaderWaves)) void scan_output_kernel(
       store_chunk(st[0], ra);
       if (NC > 1) load_chunk(rb, m0 + 1);
       if (NC > 2) load_chunk(ra, m0 + 2);
-      __syncthreads();
+      lds_barrier();
       for (int ch = 0; ch < NC; ch += 2) {
         if (ch + 1 < NC) {
           store_chunk(st[NBUF - 1], rb);
           if (ch + 3 < NC) load_chunk(rb, m0 + ch + 3);
         }
-        __syncthreads();
+        lds_barrier();
         if (ch + 1 >= NC) break;
         if (ch + 2 < NC) {
           store_chunk(st[0], ra);
           if (ch + 4 < NC) load_chunk(ra, m0 + ch + 4);
         }
-        __syncthreads();
+        lds_barrier();
       }
     } else {
       init_state();
-      __syncthreads();
+      lds_barrier();
       for (int ch = 0; ch < NC; ch += 2) {
         compute_chunk(st[0], m0 + ch);
-        __syncthreads();
+        lds_barrier();
         if (ch + 1 >= NC) break;
         compute_chunk(st[NBUF - 1], m0 + ch + 1);
-        __syncthreads();
+        lds_barrier();
       }
       store_state();
     }
@@ -372,22 +373,22 @@ __global__ __launch_bounds__(64 * (NWC + kLoaderWaves)) void scan_output_kernel(
       load_chunk(ra, m0);
       store_chunk(st[0], ra);
       if (NC > 1) load_chunk(ra, m0 + 1);
-      __syncthreads();
+      lds_barrier();
       for (int ch = 0; ch < NC; ++ch) {
-        __syncthreads();
+        lds_barrier();
         if (ch + 1 < NC) {
           store_chunk(st[0], ra);
           if (ch + 2 < NC) load_chunk(ra, m0 + ch + 2);
         }
-        __syncthreads();
+        lds_barrier();
       }
     } else {
       init_state();
-      __syncthreads();
+      lds_barrier();
       for (int ch = 0; ch < NC; ++ch) {
         compute_chunk(st[0], m0 + ch);
-        __syncthreads();
-        __syncthreads();
+        lds_barrier();
+        lds_barrier();
       }
       store_state();
     }

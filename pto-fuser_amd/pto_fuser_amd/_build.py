@@ -23,8 +23,12 @@ LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 ARCH = os.environ.get("PF_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops is disabled: the compiler must not form v_pk_{add,mul,fma}_f32 on its own.
+# The iterative-ILP machine scheduler issues the LDS operand reads of the scan's MFMA chains
+# several instructions ahead (the default strategy serialises every MFMA behind its own read,
+# which leaves a one-wave-per-SIMD kernel latency-bound).
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
-               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
 
 
 def _hipcc() -> str:
