@@ -1,0 +1,105 @@
+"""The C-ABI boundary, without a GPU: the built library loads, exports every entry point that
+include/*.h declares, the ctypes bindings agree with the header's parameter lists, and the
+host-side contract checks (status codes, workspace sizing) behave as documented.  Nothing here
+launches a kernel."""
+import glob
+import os
+import re
+
+import pytest
+
+from pto_fuser_amd import _build, _hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    """name -> parameter count, for every function prototype in include/*.h."""
+    out = {}
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", " ", open(h).read(), flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        for m in re.finditer(r"\b(pf_\w+)\s*\(([^;{)]*)\)\s*;", text):
+            params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+            out[m.group(1)] = len(params)
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    _build.ensure_built()
+    return _hip.load()
+
+
+def test_header_declares_entry_points():
+    fns = _header_functions()
+    for name in ("pf_gdn_exec", "pf_gdn_setup", "pf_gdn_teardown", "pf_tri_inv_exec",
+                 "pf_kkt_inv_exec", "pf_gdn_chunk_local_exec", "pf_gdn_scan_output_exec"):
+        assert name in fns, name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    fns = _header_functions()
+    missing = [n for n in fns if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_bindings_match_header_arity(lib):
+    fns = _header_functions()
+    assert set(_hip.SIGNATURES) == set(fns), (set(_hip.SIGNATURES) ^ set(fns))
+    for name, (_, argtypes) in _hip.SIGNATURES.items():
+        assert len(argtypes) == fns[name], f"{name}: binding has {len(argtypes)} args, header {fns[name]}"
+
+
+def test_status_strings_and_version(lib):
+    assert lib.pf_abi_version() >= 1
+    assert _hip.status_text(_hip.PF_OK) == "ok"
+    assert "argument" in _hip.status_text(_hip.PF_ERR_ARG)
+    assert "workspace" in _hip.status_text(_hip.PF_ERR_WORKSPACE)
+
+
+def test_workspace_sizing_contract(lib):
+    # T (bf16) + P (bf16) + G (fp32), each 256-byte aligned
+    M = 4 * 16 * 64
+    want = 2 * ((M * 64 * 64 * 2 + 255) // 256 * 256) + (M * 64 * 4 + 255) // 256 * 256
+    assert lib.pf_gdn_workspace_bytes(4, 16, 4096, 64, 128, 128, _hip.PF_DTYPE_BF16) == want
+    # unsupported shapes / dtypes report size 0 and setup refuses them
+    assert lib.pf_gdn_workspace_bytes(1, 1, 100, 64, 128, 128, 1) == 0      # T % C != 0
+    assert lib.pf_gdn_workspace_bytes(1, 1, 128, 32, 128, 128, 1) == 0      # C != 64
+    assert lib.pf_gdn_workspace_bytes(1, 1, 128, 64, 64, 128, 1) == 0       # DK != 128
+    assert lib.pf_gdn_workspace_bytes(1, 1, 128, 64, 128, 128, 7) == 0      # bad dtype
+    assert not lib.pf_gdn_setup(1, 1, 100, 64, 128, 128, 1)
+
+
+def test_exec_rejects_contract_violations_before_launch(lib):
+    """Bad shapes, null pointers and missing workspaces return negative codes; nothing is
+    enqueued (the calls are safe without a device)."""
+    st = lib.pf_gdn_exec(None, None, None, None, None, None, None, None,
+                         1, 1, 128, 64, 128, 128, 1, 0.1, None, None)
+    assert st == _hip.PF_ERR_WORKSPACE
+    st = lib.pf_gdn_exec(None, None, None, None, None, None, None, None,
+                         1, 1, 100, 64, 128, 128, 1, 0.1, None, None)
+    assert st == _hip.PF_ERR_ARG
+    assert lib.pf_tri_inv_exec(None, None, 4, 64, None) == _hip.PF_ERR_ARG
+    assert lib.pf_tri_inv_exec(1, 1, 4, 128, None) == _hip.PF_ERR_ARG      # unsupported C
+    assert lib.pf_kkt_inv_exec(None, None, None, None, None, 4, 64, 128, 1, 0, None) == _hip.PF_ERR_ARG
+    assert lib.pf_gdn_chunk_local_exec(None, None, None, None, 1, 1, 128, 64, 128, 128, 1,
+                                       None, None) == _hip.PF_ERR_WORKSPACE
+    assert lib.pf_gdn_scan_output_exec(None, None, None, None, None, None, None, 1, 1, 128, 64,
+                                       128, 128, 1, 0.1, None, None) == _hip.PF_ERR_WORKSPACE
+
+
+def test_ops_validate_on_host():
+    torch = pytest.importorskip("torch")
+    from pto_fuser_amd import gdn_chunk_forward, kkt_inverse, tri_inv
+    q = torch.zeros(1, 1, 64, 128)
+    with pytest.raises(ValueError, match="HIP device"):
+        gdn_chunk_forward(q, q, q, torch.zeros(1, 1, 64))
+    with pytest.raises(ValueError, match="multiple of the chunk"):
+        gdn_chunk_forward(torch.zeros(1, 1, 65, 128), q, q, torch.zeros(1, 1, 65))
+    with pytest.raises(ValueError, match="unsupported shape"):
+        gdn_chunk_forward(torch.zeros(1, 1, 64, 64), q, q, torch.zeros(1, 1, 64))
+    with pytest.raises(ValueError):
+        tri_inv(torch.zeros(2, 64, 32))
+    with pytest.raises(ValueError):
+        kkt_inverse(torch.zeros(64, 128), None, torch.zeros(64), chunk_size=32)
