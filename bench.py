@@ -37,6 +37,24 @@ PEAK_BF16 = 2.5e15         # dense bf16 MFMA, flop/s
 PEAK_FP32 = 157.3e12       # dense fp32 MFMA, flop/s
 METRIC = "GDN chunked-forward tokens/sec at B=4,H=16,T=4096 bf16; % MFMA/HBM roofline"
 
+# HBM bytes per launch at WORKLOAD, measured with two rocprofv3 counter passes over this script
+# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch; profiles/hbm_traffic_gdn_forward.md gives the
+# commands) and scaled by what the same counters read for a plain 256 MiB device copy
+# (FETCH_SIZE x2.0, WRITE_SIZE x1.0).  A counter run cannot happen inside the timed bench, so the
+# figures are recorded here and must be re-measured whenever a kernel's memory access changes.
+COUNTER_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
+MEASURED_KIB = {
+    "scan_output": {"FETCH_SIZE": 132193.7, "WRITE_SIZE": 135168.0},
+    "chunk_local": {"FETCH_SIZE": 66619.3, "WRITE_SIZE": 66567.9},
+}
+
+
+def measured_traffic(kernel):
+    kib = MEASURED_KIB.get(kernel)
+    if kib is None:
+        return None
+    return int(sum(kib[c] * COUNTER_SCALE[c] * 1024 for c in kib))
+
 
 def stage_model(B, H, T, C, DK, DV, esize):
     """Algorithmic flops and HBM bytes per launch of the two kernels.
@@ -177,7 +195,10 @@ def main(argv=None) -> int:
     dom = max(stages, key=lambda n: stages[n]["avg_ms"])
     ds = stages[dom]
     roofline = {"kernel": dom, "bound": "hbm", "achieved": ds["hbm_GBps"],
-                "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": ds["hbm_frac"], "traffic": None}
+                "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": ds["hbm_frac"],
+                "traffic": measured_traffic(dom), "algorithmic_bytes": ds["bytes"]}
+    for name in stages:
+        stages[name]["traffic"] = measured_traffic(name)
     total_bytes = sum(model[n]["bytes"] for n in model)
     total_flops = sum(model[n]["flops"] for n in model)
 
