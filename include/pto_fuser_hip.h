@@ -94,6 +94,47 @@ int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_o
  * ------------------------------------------------------------------------------------------ */
 int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Stage kernels of the compile stack's fused nodes.  No workspace (the reference's setup /
+ * teardown pairs have nothing to hold here).  Supported (C, D): C in {16, 32, 64, 128} (bf16
+ * needs C >= 32), D in {64, 128}.
+ *
+ * Row addressing shared by the gated-qk stage: chunk m = c*H + h of an [nc*C, H, D] token
+ * layout holds rows (c*C + i)*H + h, i < C.  H = 1 is the native [M, C, D] batch (M = nc).
+ * ------------------------------------------------------------------------------------------ */
+
+/* Gated a bᵀ:  L[m,i,j] = (a'_i · b'_j) · exp(min(g_i + log beta_i − g_j, 0)) · mask_ij
+ *   a' = a ⊙ a_scale, b' = b ⊙ b_scale when the scales are given (fp32, same addressing as a/b).
+ *   Replaces kkt_exec / kkt_exec_v2 (kkt_fused_lib.cpp:105-135; recipes kkt_gated, gated_qk and
+ *   their _native / _native_v2 forms, fused.py:200-290) and, with scales and g = beta = NULL,
+ *   pro_exec / pro_exec_v2 (prologue_fused_lib.cpp; recipes qk_prologue*, fused.py:293-340).
+ *   a, b: dtype, rows of D; g, beta: fp32 [nc*C, H] or NULL (0 / 1); mask: [C,C] fp32 or NULL
+ *   (then causal = 1 keeps i >= j, 0 keeps i > j); L: [nc*C, H, C] in out_dtype (fp32 or bf16). */
+int pf_gated_qk_exec(const void* a, const void* b, const float* a_scale, const float* b_scale,
+                     const float* g, const float* beta, const float* mask, void* L, int nc, int H,
+                     int C, int D, int dtype, int causal, int out_dtype, void* stream);
+
+/* chunk_o flash: o[m] = causal_incl( (q'kᵀ') · exp(min(g_i + log beta_i − g_j, 0)) ) · v[m], the
+ * score never leaving the chip.  q' = q ⊙ q_scale, k' = k ⊙ k_scale when given (per-channel gate,
+ * the qkvp form).  Replaces qkv_exec / qkv_exec_v2 (qkv_fused_lib.cpp:123-165; recipes
+ * qkv_flash_native*, fused.py:353-395) and qkvp_exec* (qkv_prologue_fused_lib.cpp; recipes
+ * qkvp_flash_native*, fused.py:411-444).  q, k, v [M,C,D] dtype; scales [M,C,D] fp32 or NULL;
+ * g, beta [M,C] fp32 or NULL; o [M,C,D] fp32. */
+int pf_qkv_flash_exec(const void* q, const void* k, const void* v, const float* q_scale,
+                      const float* k_scale, const float* g, const float* beta, float* o, int M,
+                      int C, int D, int dtype, void* stream);
+
+/* Resident-state chunk recurrence (chunk_h_scan).  Per (b,h), chunk c:
+ *   h_out[b,c,h] = S;   S = decay[b,h,c] ⊙ S + k_cᵀ (u_c − w_c S)
+ * decay is a scalar per chunk ([B,H,nc], perdim = 0) or scales state row d ([B,H,nc,D],
+ * perdim = 1).  Replaces scan_exec (scan_lib.cpp:81-99, scan_fused.h:198-262; per-dim form
+ * :143-180; recipe chunk_h_scan, fused.py:168-182), which is fixed to C = D = 128 and starts from
+ * zero: here h0 [B,H,D,D] fp32 (or NULL = zero) is accepted.  w, u, k [B,nc,C,H,D] dtype;
+ * h_out [B,nc,H,D,D] in out_dtype; final_state [B,H,D,D] fp32 or NULL. */
+int pf_scan_exec(const void* w, const void* u, const void* k, const float* decay,
+                 const float* h0, void* h_out, float* final_state, int B, int H, int nc, int C,
+                 int D, int dtype, int perdim, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

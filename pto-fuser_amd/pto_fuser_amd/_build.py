@@ -11,6 +11,7 @@ import glob
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 from typing import List, Optional
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -26,9 +27,10 @@ ARCH = os.environ.get("PF_OFFLOAD_ARCH", "gfx950")
 # The iterative-ILP machine scheduler issues the LDS operand reads of the scan's MFMA chains
 # several instructions ahead (the default strategy serialises every MFMA behind its own read,
 # which leaves a one-wave-per-SIMD kernel latency-bound).
-HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
+OBJ_DIR = os.path.join(ROOT, "_build")
 
 
 def _hipcc() -> str:
@@ -46,19 +48,35 @@ def headers() -> List[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h")))
 
 
-def build(verbose: bool = False, out: Optional[str] = None) -> str:
-    """Compile every HIP source into the shared library; raises RuntimeError with the compiler
-    output on failure.  Returns the library path."""
-    out = out or LIB_PATH
-    os.makedirs(os.path.dirname(out), exist_ok=True)
-    tmp = out + f".tmp{os.getpid()}"
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, *sources(), "-o", tmp]
+def _run(cmd: List[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"libptofuser_hip build failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, out)
+        raise RuntimeError(f"libptofuser_hip build failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+
+
+def build(verbose: bool = False, out: Optional[str] = None) -> str:
+    """Compile every HIP source to an object (one hipcc per translation unit, in parallel), then
+    link the shared library; raises RuntimeError with the compiler output on failure.  Returns
+    the library path."""
+    out = out or LIB_PATH
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    obj_dir = os.path.join(OBJ_DIR, str(os.getpid()))
+    os.makedirs(obj_dir, exist_ok=True)
+    hipcc = _hipcc()
+    srcs = sources()
+    objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", "8"))))
+    try:
+        with ThreadPoolExecutor(jobs) as pool:
+            list(pool.map(lambda so: _run([hipcc, *HIPCC_FLAGS, "-I", INCLUDE, "-c", so[0], "-o", so[1]],
+                                          verbose), zip(srcs, objs)))
+        tmp = out + f".tmp{os.getpid()}"
+        _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp], verbose)
+        os.replace(tmp, out)
+    finally:
+        shutil.rmtree(obj_dir, ignore_errors=True)
     return out
 
 

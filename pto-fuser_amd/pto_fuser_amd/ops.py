@@ -171,6 +171,132 @@ def kkt_inverse(k: torch.Tensor, g: Optional[torch.Tensor], beta: torch.Tensor,
     return (Tm, A) if return_A else Tm
 
 
+STAGE_C = (16, 32, 64, 128)
+STAGE_D = (64, 128)
+
+
+def _stage_shape(C: int, D: int, dtype: torch.dtype) -> None:
+    if C not in STAGE_C or D not in STAGE_D or (dtype == torch.bfloat16 and C < 32):
+        raise ValueError(f"unsupported stage shape C={C} D={D} {dtype} (C in {STAGE_C}, "
+                         f"D in {STAGE_D}; bfloat16 needs C >= 32)")
+
+
+def _on_device(t: torch.Tensor, name: str) -> torch.device:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a tensor on a HIP device")
+    return t.device
+
+
+def gated_qk(a: torch.Tensor, b: torch.Tensor, g: Optional[torch.Tensor] = None,
+             beta: Optional[torch.Tensor] = None, *, chunk_size: int, heads: int = 1,
+             causal: bool = True, mask: Optional[torch.Tensor] = None,
+             a_scale: Optional[torch.Tensor] = None, b_scale: Optional[torch.Tensor] = None,
+             out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Gated a bᵀ per chunk: L_ij = (a'_i·b'_j)·exp(min(g_i + log β_i − g_j, 0))·mask_ij.
+
+    ``heads = 1``: a, b are the native batch [M, C, D] (any shape flattening to it), g/β [M, C];
+    L is [M, C, C].  ``heads = H``: a, b are the token layout [nc*C, H, D] (= [1, T, H, D]),
+    g/β [nc*C, H], L is [nc*C, H, C] — the two layouts of kkt_fused_lib.cpp's callers
+    (fused.py:200-290).  ``mask`` [C, C] float32 overrides ``causal`` (True: i ≥ j, False: i > j).
+    ``a_scale``/``b_scale`` (float32, a's/b's shape) multiply the operands first: the per-channel
+    prologue of qk_prologue (fused.py:293-340).  g, β, mask, scales may be None."""
+    dev = _on_device(a, "a")
+    C, H, D = int(chunk_size), int(heads), a.shape[-1]
+    code = _dtype_code(a.dtype)
+    _stage_shape(C, D, a.dtype)
+    n = a.numel() // D
+    if n % (C * H):
+        raise ValueError(f"{n} rows do not split into chunks of {C} tokens x {H} heads")
+    nc = n // (C * H)
+    for name, t in (("a", a), ("b", b)):
+        _require(t.reshape(n, D) if t.is_contiguous() else t, name, (n, D), a.dtype, dev)
+    for name, t in (("a_scale", a_scale), ("b_scale", b_scale)):
+        if t is not None:
+            _require(t.reshape(n, D) if t.is_contiguous() else t, name, (n, D), torch.float32, dev)
+    for name, t in (("g", g), ("beta", beta)):
+        if t is not None:
+            _require(t.reshape(n) if t.is_contiguous() else t, name, (n,), torch.float32, dev)
+    _require(mask, "mask", (C, C), torch.float32, dev)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"out_dtype must be float32 or bfloat16, got {out_dtype}")
+    L = torch.empty((nc, C, C) if H == 1 else (nc * C, H, C), device=dev, dtype=out_dtype)
+    st = _hip.load().pf_gated_qk_exec(
+        _hip.ptr(a), _hip.ptr(b), _hip.ptr(a_scale), _hip.ptr(b_scale), _hip.ptr(g),
+        _hip.ptr(beta), _hip.ptr(mask), _hip.ptr(L), nc, H, C, D, code, int(bool(causal)),
+        _dtype_code(out_dtype), _hip.current_stream_handle(dev))
+    _hip.check("pf_gated_qk_exec", st)
+    return L
+
+
+def qkv_flash(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: Optional[torch.Tensor] = None,
+              beta: Optional[torch.Tensor] = None, *, chunk_size: int,
+              q_scale: Optional[torch.Tensor] = None,
+              k_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """chunk_o flash, one launch: o = causal_incl((q'k'ᵀ)·exp(min(g_i + log β_i − g_j, 0)))·v.
+
+    q, k, v [M, C, D] (any shape flattening to it), float32 or bfloat16; g, β [M, C] float32 or
+    None; q_scale/k_scale [M, C, D] float32 or None (the per-channel qkvp form).  Returns o
+    [M, C, D] float32 (qkv_fused.h:62-175 semantics)."""
+    dev = _on_device(q, "q")
+    C, D = int(chunk_size), q.shape[-1]
+    code = _dtype_code(q.dtype)
+    _stage_shape(C, D, q.dtype)
+    n = q.numel() // D
+    if n % C:
+        raise ValueError(f"{n} rows do not split into chunks of {C}")
+    M = n // C
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require(t.reshape(n, D) if t.is_contiguous() else t, name, (n, D), q.dtype, dev)
+    for name, t in (("q_scale", q_scale), ("k_scale", k_scale)):
+        if t is not None:
+            _require(t.reshape(n, D) if t.is_contiguous() else t, name, (n, D), torch.float32, dev)
+    for name, t in (("g", g), ("beta", beta)):
+        if t is not None:
+            _require(t.reshape(n) if t.is_contiguous() else t, name, (n,), torch.float32, dev)
+    o = torch.empty(M, C, D, device=dev, dtype=torch.float32)
+    st = _hip.load().pf_qkv_flash_exec(
+        _hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(q_scale), _hip.ptr(k_scale), _hip.ptr(g),
+        _hip.ptr(beta), _hip.ptr(o), M, C, D, code, _hip.current_stream_handle(dev))
+    _hip.check("pf_qkv_flash_exec", st)
+    return o
+
+
+def chunk_scan(w: torch.Tensor, u: torch.Tensor, k: torch.Tensor, decay: torch.Tensor,
+               h0: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.float32,
+               output_final_state: bool = True):
+    """Resident-state chunk recurrence (chunk_h_scan, scan_fused.h:198-262).
+
+    w, u, k [B, nc, C, H, D] float32/bfloat16 (token-major); decay [B, H, nc] (scalar per chunk) or
+    [B, H, nc, D] (per key channel: row d of S scales by decay[..., d]) float32; h0 [B, H, D, D]
+    float32 or None.  Returns (h_out [B, nc, H, D, D] in ``out_dtype`` — the state *before* each
+    chunk — and the final state [B, H, D, D] float32 or None)."""
+    dev = _on_device(w, "w")
+    if w.dim() != 5:
+        raise ValueError(f"w must be [B, nc, C, H, D], got {tuple(w.shape)}")
+    B, nc, C, H, D = w.shape
+    code = _dtype_code(w.dtype)
+    _stage_shape(C, D, w.dtype)
+    for name, t in (("w", w), ("u", u), ("k", k)):
+        _require(t, name, (B, nc, C, H, D), w.dtype, dev)
+    if decay.dim() == 3:
+        perdim = 0
+        _require(decay, "decay", (B, H, nc), torch.float32, dev)
+    else:
+        perdim = 1
+        _require(decay, "decay", (B, H, nc, D), torch.float32, dev)
+    _require(h0, "h0", (B, H, D, D), torch.float32, dev)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"out_dtype must be float32 or bfloat16, got {out_dtype}")
+    h_out = torch.empty(B, nc, H, D, D, device=dev, dtype=out_dtype)
+    final = torch.empty(B, H, D, D, device=dev, dtype=torch.float32) if output_final_state else None
+    st = _hip.load().pf_scan_exec(
+        _hip.ptr(w), _hip.ptr(u), _hip.ptr(k), _hip.ptr(decay), _hip.ptr(h0), _hip.ptr(h_out),
+        _hip.ptr(final), B, H, nc, C, D, code, perdim, _dtype_code(out_dtype),
+        _hip.current_stream_handle(dev))
+    _hip.check("pf_scan_exec", st)
+    return h_out, final
+
+
 def tri_inv(A: torch.Tensor) -> torch.Tensor:
     """(I + A)^-1 of strictly-lower A [M, C, C] float32 (upper part ignored), C in 16..64."""
     if A.dim() != 3 or A.shape[1] != A.shape[2]:

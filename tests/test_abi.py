@@ -87,6 +87,23 @@ def test_exec_rejects_contract_violations_before_launch(lib):
                                        None, None) == _hip.PF_ERR_WORKSPACE
     assert lib.pf_gdn_scan_output_exec(None, None, None, None, None, None, None, 1, 1, 128, 64,
                                        128, 128, 1, 0.1, None, None) == _hip.PF_ERR_WORKSPACE
+    # stage kernels: null operands, unsupported (C, D, dtype) and bad output dtypes
+    assert lib.pf_gated_qk_exec(None, None, None, None, None, None, None, None, 1, 1, 64, 128,
+                                1, 1, 0, None) == _hip.PF_ERR_ARG
+    assert lib.pf_gated_qk_exec(1, 1, None, None, None, None, None, 1, 1, 1, 16, 128,
+                                1, 1, 0, None) == _hip.PF_ERR_ARG      # bf16 needs C >= 32
+    assert lib.pf_gated_qk_exec(1, 1, None, None, None, None, None, 1, 1, 1, 64, 96,
+                                0, 1, 0, None) == _hip.PF_ERR_ARG      # D = 96
+    assert lib.pf_gated_qk_exec(1, 1, None, None, None, None, None, 1, 1, 1, 64, 128,
+                                0, 1, 5, None) == _hip.PF_ERR_ARG      # out dtype
+    assert lib.pf_qkv_flash_exec(1, 1, None, None, None, None, None, 1, 4, 64, 128, 1,
+                                 None) == _hip.PF_ERR_ARG              # v missing
+    assert lib.pf_qkv_flash_exec(1, 1, 1, None, None, None, None, 1, 4, 256, 128, 0,
+                                 None) == _hip.PF_ERR_ARG              # C = 256
+    assert lib.pf_scan_exec(1, 1, 1, None, None, 1, None, 1, 1, 2, 64, 128, 1, 0, 0,
+                            None) == _hip.PF_ERR_ARG                   # decay missing
+    assert lib.pf_scan_exec(1, 1, 1, 1, None, 1, None, 0, 1, 2, 64, 128, 1, 0, 0,
+                            None) == _hip.PF_ERR_ARG                   # B = 0
 
 
 def test_ops_validate_on_host():

@@ -325,3 +325,29 @@ def test_error_metrics():
     x = r + np.array([0.0, 0.5, 0.0])
     assert max_abs(x, r) == 0.5 and max_rel(x, r) == 0.125
     assert abs(frob_rel(x, r) - 0.5 / np.sqrt(21.0)) < 1e-15
+
+
+def test_scan_per_channel_decay_brute_force():
+    """scan_reference with a per-channel decay vector: S <- diag(d) S + k^T (u - w S), checked
+    element by element in plain loops, and equal to the scalar form when d is constant."""
+    rng = np.random.default_rng(171)
+    B, nc, C, H, D = 1, 2, 3, 2, 4
+    w, u, k = (rng.standard_normal((B, nc, C, H, D)) for _ in range(3))
+    dec = rng.random((B, H, nc, D))
+    h0 = rng.standard_normal((B, H, D, D))
+    h_out, final = scan_reference(w, u, k, dec, h0=h0, dtype=np.float64)
+    for h in range(H):
+        S = [[h0[0, h, i, j] for j in range(D)] for i in range(D)]
+        for c in range(nc):
+            for i in range(D):
+                for j in range(D):
+                    assert abs(h_out[0, c, h, i, j] - S[i][j]) < 1e-12
+            vc = [[u[0, c, t, h, j] - sum(w[0, c, t, h, d] * S[d][j] for d in range(D))
+                   for j in range(D)] for t in range(C)]
+            S = [[dec[0, h, c, i] * S[i][j] + sum(k[0, c, t, h, i] * vc[t][j] for t in range(C))
+                  for j in range(D)] for i in range(D)]
+        assert max_abs(final[0, h], np.array(S)) < 1e-12
+    const = np.repeat(dec[..., :1], D, axis=-1)
+    hs, fs = scan_reference(w, u, k, const[..., 0], h0=h0, dtype=np.float64)
+    hp, fp = scan_reference(w, u, k, const, h0=h0, dtype=np.float64)
+    assert max_abs(hs, hp) < 1e-12 and max_abs(fs, fp) < 1e-12
