@@ -90,7 +90,7 @@ int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_o
  * registry.py:124 (`tri_inv(out, A_upper, mi, C, M, 0, cu_seqlens=None, block_dim)`), which
  * inverts strictly-upper fp16 input: this one takes the strictly-LOWER fp32 A directly.
  *   A [M,C,C] fp32 (only the strictly-lower part is read); T_out [M,C,C] fp32 = (I + A)^-1.
- *   Supported: C in {16, 32, 48, 64}.
+ *   Supported: C in {16, 32, 48, 64, 128} (the reference contract is {16, 32, 64, 128}).
  * ------------------------------------------------------------------------------------------ */
 int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream);
 

@@ -232,6 +232,7 @@ int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream) {
     case 32: pf::tri_inv_kernel<32><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
     case 48: pf::tri_inv_kernel<48><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
     case 64: pf::tri_inv_kernel<64><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
+    case 128: pf::tri_inv_kernel<128><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
     default: return PF_ERR_ARG;
   }
   return launch_status();

@@ -1,0 +1,337 @@
+"""Fused-kernel registry: the FusedNode backend (src/pto_fuser/fused.py:1-598).
+
+A ``FusedNode`` names one HIP kernel of libptofuser_hip.so that stands in for a staged
+sub-chain.  The registry maps the key to a recipe: the C entry point, the shape key, the launch
+adapter (operand layout/dtype, output allocation) and the pinned contract.  Launches go on the
+current torch stream with no host synchronisation and no allocation inside the library, so a
+fused node is capturable into a HIP graph.
+
+Keys and contracts are the reference's, so its programs and transforms name the same kernels:
+
+  chunk_h_scan                      pf_scan_exec       resident-state recurrence
+  kkt_gated, gated_qk               pf_gated_qk_exec   token layout [1, T, H, D]
+  kkt_gated_native[_v2],
+  gated_qk_native[_v2]              pf_gated_qk_exec   native batch [M, C, D]
+  qk_prologue[_v2]                  pf_gated_qk_exec   per-channel operand prescale
+  qkv_flash_native[_v2]             pf_qkv_flash_exec  chunk_o score -> output
+  qkvp_flash_native[_v2]            pf_qkv_flash_exec  per-channel chunk_o flash
+
+Differences from the reference, all deliberate:
+
+* No per-shape compilation.  The reference builds one ``.so`` per ``-D`` set with bisheng; here
+  every shape dispatches at run time onto instantiations inside the one library, so ``defines``
+  only keys the kernel cache.
+* The ``_v2`` keys (the reference's FFTS-interleave / L2-ring variants, which exist to stop its
+  intermediate scores round-tripping HBM) run the same kernels as the plain keys: the HIP kernels
+  never write the score to HBM in the first place.
+* Operand dtype: bf16 (the MI355X MFMA type) or fp32 instead of fp16.  An fp16 operand is
+  converted to bf16; fp32 operands run the fp32 MFMA path.  Gates are fp32.
+* The scan accepts any C in {16, 32, 64, 128} and D in {64, 128} (the reference is fixed to
+  C = D = 128) and returns the final state.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Callable, Dict, List, Optional, Tuple
+
+import torch
+
+from . import ops
+
+__all__ = ["FusedContract", "FusedKernel", "FusedKernelRegistry", "default_fused_registry",
+           "shared_fused_registry"]
+
+
+# --------------------------------------------------------------------------- #
+#  contract + runner
+# --------------------------------------------------------------------------- #
+@dataclass
+class FusedContract:
+    """The pinned interface of one fused kernel."""
+    in_slots: List[str]
+    in_dtypes: List[Any]
+    out_names: List[str]
+    out_dtype: Any
+    notes: str = ""
+
+
+class FusedKernel:
+    """One recipe bound to one shape key.  ``run`` adapts the operands and launches on the
+    current stream; there is no per-kernel workspace to set up or tear down (the stage kernels
+    keep their intermediates on chip), so ``close`` has nothing to free."""
+
+    def __init__(self, key: str, launch: Callable, entry: str) -> None:
+        self.key, self._launch, self.entry = key, launch, entry
+
+    def run(self, inputs: List[torch.Tensor], params: dict) -> List[torch.Tensor]:
+        return self._launch(inputs, params)
+
+    def close(self) -> None:
+        pass
+
+
+@dataclass
+class _Recipe:
+    entry: str                                   # C entry point in libptofuser_hip.so
+    defines: Callable[[dict], Dict[str, int]]    # params -> shape key
+    launch: Callable                             # (inputs, params) -> [outputs]
+    contract: FusedContract
+
+
+class FusedKernelRegistry:
+    def __init__(self) -> None:
+        self._recipes: Dict[str, _Recipe] = {}
+        self._cache: Dict[Tuple, FusedKernel] = {}
+
+    def register(self, key: str, recipe: _Recipe) -> None:
+        if key in self._recipes:
+            raise ValueError(f"fused kernel {key!r} already registered")
+        self._recipes[key] = recipe
+
+    def keys(self) -> List[str]:
+        return list(self._recipes)
+
+    def contract(self, key: str) -> FusedContract:
+        if key not in self._recipes:
+            raise KeyError(f"no fused kernel registered under {key!r}")
+        return self._recipes[key].contract
+
+    def kernel(self, key: str, params: dict) -> FusedKernel:
+        if key not in self._recipes:
+            raise KeyError(f"no fused kernel registered under {key!r}")
+        r = self._recipes[key]
+        ck = (key, tuple(sorted(r.defines(params).items())))
+        if ck not in self._cache:
+            self._cache[ck] = FusedKernel(key, r.launch, r.entry)
+        return self._cache[ck]
+
+    def run(self, key: str, inputs: List[torch.Tensor], params: dict) -> List[torch.Tensor]:
+        return self.kernel(key, params).run(inputs, params)
+
+    def close(self) -> None:
+        for k in self._cache.values():
+            k.close()
+        self._cache.clear()
+
+
+# --------------------------------------------------------------------------- #
+#  operand adapters
+# --------------------------------------------------------------------------- #
+def _operand_dtype(*ts: torch.Tensor) -> torch.dtype:
+    """fp32 if any operand is fp32 or wider, else bf16."""
+    return torch.float32 if any(t.dtype in (torch.float32, torch.float64) for t in ts) \
+        else torch.bfloat16
+
+
+def _op(t: torch.Tensor, dtype: torch.dtype, shape=None) -> torch.Tensor:
+    t = t.to(dtype) if t.dtype != dtype else t
+    if shape is not None:
+        t = t.reshape(shape)
+    return t.contiguous()
+
+
+def _f32(t: Optional[torch.Tensor], shape=None) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    return _op(t, torch.float32, shape)
+
+
+def _native_dims(a: torch.Tensor, params: dict) -> Tuple[int, int, int]:
+    """(M, C, D) of a native [M, C, D] operand from the node params (M = nc * H)."""
+    M = int(params["nc"]) * int(params["H"])
+    D = int(params.get("D", a.shape[-1]))
+    C = int(params.get("C", a.numel() // (M * D)))
+    if M * C * D != a.numel():
+        raise ValueError(f"operand of {a.numel()} elements is not [M={M}, C={C}, D={D}]")
+    return M, C, D
+
+
+# --------------------------------------------------------------------------- #
+#  chunk_h_scan
+# --------------------------------------------------------------------------- #
+def _scan_launch(inputs, params) -> List[torch.Tensor]:
+    w, u, k, decay = inputs          # [B,nc,C,H,D] x3; decay [B,H,nc] or [B,H,nc,D]
+    B, H, nc = int(params["B"]), int(params["H"]), int(params["nc"])
+    dt = _operand_dtype(w, u, k)
+    D = w.shape[-1]
+    C = w.numel() // (B * nc * H * D)
+    shape = (B, nc, C, H, D)
+    dshape = (B, H, nc, D) if params.get("perdim_decay") else (B, H, nc)
+    h_out, final = ops.chunk_scan(_op(w, dt, shape), _op(u, dt, shape), _op(k, dt, shape),
+                                  _f32(decay, dshape), out_dtype=dt)
+    return [h_out, final.to(dt)]
+
+
+# --------------------------------------------------------------------------- #
+#  gated a·bᵀ (kkt / chunk_o score / per-channel prologue)
+# --------------------------------------------------------------------------- #
+def _gated_token_layout(a, b, g_sum, beta, params, causal) -> List[torch.Tensor]:
+    """Token layout: a, b [1, T, H, D]; g_sum, beta [1, T, H] -> L [T, H, C]."""
+    nc, H = int(params["nc"]), int(params["H"])
+    D = a.shape[-1]
+    T = a.numel() // (H * D)
+    C = T // nc
+    dt = _operand_dtype(a, b)
+    L = ops.gated_qk(_op(a, dt, (T, H, D)), _op(b, dt, (T, H, D)), _f32(g_sum, (T, H)),
+                     _f32(beta, (T, H)), chunk_size=C, heads=H, causal=causal, out_dtype=dt)
+    return [L]
+
+
+def _kkt_launch(inputs, params):
+    k, g_sum, beta = inputs
+    return _gated_token_layout(k, k, g_sum, beta, params, causal=False)
+
+
+def _gated_qk_launch(inputs, params):
+    a, b, g_sum, beta = inputs
+    return _gated_token_layout(a, b, g_sum, beta, params, causal=params.get("causal", True))
+
+
+def _gated_native(a, b, g, beta, params, causal) -> List[torch.Tensor]:
+    """Native layout: a, b [M, C, D]; g, beta [M, C] -> L [M, C, C]."""
+    M, C, D = _native_dims(a, params)
+    dt = _operand_dtype(a, b)
+    L = ops.gated_qk(_op(a, dt, (M, C, D)), _op(b, dt, (M, C, D)), _f32(g, (M, C)),
+                     _f32(beta, (M, C)), chunk_size=C, causal=causal, out_dtype=dt)
+    return [L]
+
+
+def _kkt_native_launch(inputs, params):
+    k, g_native, beta_native = inputs
+    return _gated_native(k, k, g_native, beta_native, params, causal=False)
+
+
+def _gated_qk_native_launch(inputs, params):
+    a, b, g_native, beta_native = inputs
+    return _gated_native(a, b, g_native, beta_native, params, causal=params.get("causal", True))
+
+
+def _prologue_launch(inputs, params):
+    """L = tril((q ⊙ P)(k ⊙ invP)ᵀ), causal incl. the diagonal (prologue_fused.h:37-107)."""
+    q, k, P, invP = inputs
+    M, C, D = _native_dims(q, params)
+    dt = _operand_dtype(q, k)
+    L = ops.gated_qk(_op(q, dt, (M, C, D)), _op(k, dt, (M, C, D)), chunk_size=C, causal=True,
+                     a_scale=_f32(P, (M, C, D)), b_scale=_f32(invP, (M, C, D)), out_dtype=dt)
+    return [L]
+
+
+# --------------------------------------------------------------------------- #
+#  chunk_o flash
+# --------------------------------------------------------------------------- #
+def _flash_dims(q, v, params):
+    M, C, D = _native_dims(q, params)
+    DV = int(params.get("DV", D))
+    if DV != D or v.numel() != M * C * DV:
+        raise ValueError(f"chunk_o flash needs v of shape [M, C, D] with DV == D (got DV={DV})")
+    return M, C, D
+
+
+def _qkv_launch(inputs, params):
+    """o = causal((q·kᵀ)·exp(min(g_i + log β_i − g_j, 0)))·v, fp32 (qkv_fused.h:62-175)."""
+    q, k, v, g_native, beta_native = inputs
+    M, C, D = _flash_dims(q, v, params)
+    dt = _operand_dtype(q, k, v)
+    o = ops.qkv_flash(_op(q, dt, (M, C, D)), _op(k, dt, (M, C, D)), _op(v, dt, (M, C, D)),
+                      _f32(g_native, (M, C)), _f32(beta_native, (M, C)), chunk_size=C)
+    return [o]
+
+
+def _qkvp_launch(inputs, params):
+    """o = tril((q ⊙ coef_ag)·(k ⊙ coef_bg)ᵀ)·v, fp32 (qkv_prologue_fused.h:99-187)."""
+    q, k, v, coef_ag, coef_bg = inputs
+    M, C, D = _flash_dims(q, v, params)
+    dt = _operand_dtype(q, k, v)
+    o = ops.qkv_flash(_op(q, dt, (M, C, D)), _op(k, dt, (M, C, D)), _op(v, dt, (M, C, D)),
+                      chunk_size=C, q_scale=_f32(coef_ag, (M, C, D)),
+                      k_scale=_f32(coef_bg, (M, C, D)))
+    return [o]
+
+
+# --------------------------------------------------------------------------- #
+#  the default registry
+# --------------------------------------------------------------------------- #
+def _shape_key(*names):
+    return lambda p: {n: p[n] for n in names if n in p}
+
+
+_BF, _F32 = torch.bfloat16, torch.float32
+
+
+def default_fused_registry() -> FusedKernelRegistry:
+    reg = FusedKernelRegistry()
+    reg.register("chunk_h_scan", _Recipe(
+        entry="pf_scan_exec", defines=_shape_key("B", "H", "nc", "perdim_decay"),
+        launch=_scan_launch,
+        contract=FusedContract(
+            in_slots=["w", "u", "k", "decay"], in_dtypes=[_BF, _BF, _BF, _F32],
+            out_names=["h_out", "final"], out_dtype=_BF,
+            notes="resident-state chunk recurrence; w/u/k [B,nc,C,H,D]; decay [B,H,nc] scalar "
+                  "or [B,H,nc,D] per key channel (perdim_decay=True); C in {16,32,64,128}, "
+                  "D in {64,128}; fp32 operands run fp32 end to end")))
+    reg.register("kkt_gated", _Recipe(
+        entry="pf_gated_qk_exec", defines=_shape_key("nc", "H"), launch=_kkt_launch,
+        contract=FusedContract(
+            in_slots=["k", "g_sum", "beta"], in_dtypes=[_BF, _F32, _F32],
+            out_names=["L"], out_dtype=_BF,
+            notes="gated strict-lower k·kᵀ on the token layout k [1,T,H,D] -> L [T,H,C]")))
+    reg.register("gated_qk", _Recipe(
+        entry="pf_gated_qk_exec", defines=_shape_key("nc", "H", "causal"),
+        launch=_gated_qk_launch,
+        contract=FusedContract(
+            in_slots=["a", "b", "g_sum", "beta"], in_dtypes=[_BF, _BF, _F32, _F32],
+            out_names=["L"], out_dtype=_BF,
+            notes="gated a·bᵀ on the token layout a,b [1,T,H,D]; chunk_o score = "
+                  "(q, k, beta=1, causal)")))
+    for key, launch, slots, note in (
+            ("kkt_gated_native", _kkt_native_launch, ["k", "g_native", "beta_native"],
+             "native kkt (k·kᵀ, real beta, strict lower); k [M,C,D], g/beta [M,C]"),
+            ("gated_qk_native", _gated_qk_native_launch,
+             ["a", "b", "g_native", "beta_native"],
+             "native a·bᵀ + gate/mask epilogue; chunk_o Aqk = (q, k, beta=1, causal)")):
+        for suffix in ("", "_v2"):
+            reg.register(key + suffix, _Recipe(
+                entry="pf_gated_qk_exec", defines=_shape_key("nc", "H", "C", "D", "causal"),
+                launch=launch,
+                contract=FusedContract(
+                    in_slots=list(slots), in_dtypes=[_BF] * (len(slots) - 2) + [_F32, _F32],
+                    out_names=["L"], out_dtype=_BF,
+                    notes=note + ("; same kernel as the plain key (the score never leaves the "
+                                  "chip in either)" if suffix else ""))))
+    for suffix in ("", "_v2"):
+        reg.register("qk_prologue" + suffix, _Recipe(
+            entry="pf_gated_qk_exec", defines=_shape_key("nc", "H", "C", "D"),
+            launch=_prologue_launch,
+            contract=FusedContract(
+                in_slots=["q", "k", "P", "invP"], in_dtypes=[_BF, _BF, _F32, _F32],
+                out_names=["L"], out_dtype=_BF,
+                notes="per-channel prologue tril((q⊙P)·(k⊙invP)ᵀ); q/k/P/invP [M,C,D], "
+                      "L [M,C,C]")))
+    qkv = FusedContract(
+        in_slots=["q", "k", "v", "g_native", "beta_native"],
+        in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
+        notes="chunk_o flash: o = tril((q·kᵀ)·exp(min(g_i-g_j,0)))·v in one launch; "
+              "q/k/v [M,C,D], o [M,C,D] fp32")
+    qkvp = FusedContract(
+        in_slots=["q", "k", "v", "coef_ag", "coef_bg"],
+        in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
+        notes="per-channel chunk_o flash: o = tril((q⊙coef_ag)·(k⊙coef_bg)ᵀ)·v in one launch")
+    for suffix in ("", "_v2"):
+        reg.register("qkv_flash_native" + suffix, _Recipe(
+            entry="pf_qkv_flash_exec", defines=_shape_key("nc", "H", "C", "D", "DV"),
+            launch=_qkv_launch, contract=qkv))
+        reg.register("qkvp_flash_native" + suffix, _Recipe(
+            entry="pf_qkv_flash_exec", defines=_shape_key("nc", "H", "C", "D", "DV"),
+            launch=_qkvp_launch, contract=qkvp))
+    return reg
+
+
+_DEFAULT: Optional[FusedKernelRegistry] = None
+
+
+def shared_fused_registry() -> FusedKernelRegistry:
+    """Process-wide registry, shared by every executor (and across graph capture/replay)."""
+    global _DEFAULT
+    if _DEFAULT is None:
+        _DEFAULT = default_fused_registry()
+    return _DEFAULT

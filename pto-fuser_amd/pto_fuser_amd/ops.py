@@ -172,6 +172,7 @@ def kkt_inverse(k: torch.Tensor, g: Optional[torch.Tensor], beta: torch.Tensor,
 
 
 STAGE_C = (16, 32, 64, 128)
+TRI_INV_C = (16, 32, 48, 64, 128)
 STAGE_D = (64, 128)
 
 
@@ -298,12 +299,12 @@ def chunk_scan(w: torch.Tensor, u: torch.Tensor, k: torch.Tensor, decay: torch.T
 
 
 def tri_inv(A: torch.Tensor) -> torch.Tensor:
-    """(I + A)^-1 of strictly-lower A [M, C, C] float32 (upper part ignored), C in 16..64."""
+    """(I + A)^-1 of strictly-lower A [M, C, C] float32 (upper part ignored), C in TRI_INV_C."""
     if A.dim() != 3 or A.shape[1] != A.shape[2]:
         raise ValueError(f"A must be [M, C, C], got {tuple(A.shape)}")
     M, C, _ = A.shape
-    if C not in (16, 32, 48, 64):
-        raise ValueError(f"tri_inv supports C in (16, 32, 48, 64), got {C}")
+    if C not in TRI_INV_C:
+        raise ValueError(f"tri_inv supports C in {TRI_INV_C}, got {C}")
     if A.dtype != torch.float32 or A.device.type != "cuda" or not A.is_contiguous():
         raise ValueError("A must be a contiguous float32 tensor on a HIP device")
     out = torch.empty_like(A)

@@ -81,7 +81,7 @@ def test_exec_rejects_contract_violations_before_launch(lib):
                          1, 1, 100, 64, 128, 128, 1, 0.1, None, None)
     assert st == _hip.PF_ERR_ARG
     assert lib.pf_tri_inv_exec(None, None, 4, 64, None) == _hip.PF_ERR_ARG
-    assert lib.pf_tri_inv_exec(1, 1, 4, 128, None) == _hip.PF_ERR_ARG      # unsupported C
+    assert lib.pf_tri_inv_exec(1, 1, 4, 96, None) == _hip.PF_ERR_ARG       # unsupported C
     assert lib.pf_kkt_inv_exec(None, None, None, None, None, 4, 64, 128, 1, 0, None) == _hip.PF_ERR_ARG
     assert lib.pf_gdn_chunk_local_exec(None, None, None, None, 1, 1, 128, 64, 128, 128, 1,
                                        None, None) == _hip.PF_ERR_WORKSPACE

@@ -36,7 +36,7 @@ def _oracle(inp, dtype=np.float64):
     return gdn_reference(x["q"], x["k"], x["v"], x["beta"], g, h0=x["h0"], C=64, dtype=dtype)
 
 
-@pytest.mark.parametrize("C", [16, 32, 48, 64])
+@pytest.mark.parametrize("C", [16, 32, 48, 64, 128])
 def test_tri_inv_matches_oracle(C):
     announce(f"tri_inv C={C} M=96")
     rng = np.random.default_rng(C)
