@@ -152,14 +152,13 @@ def main(argv=None) -> int:
         if ev is not None:
             ev[0].record(stream)
         st = lib.pf_gdn_chunk_local_exec(P["q"], P["k"], P["beta"], P["g"], B, H, T, C, DK, DV,
-                                         code, ws.handle, sh)
+                                         code, scale, ws.handle, sh)
         if st:
             _hip.check("pf_gdn_chunk_local_exec", st)
         if ev is not None:
             ev[1].record(stream)
         st = lib.pf_gdn_scan_output_exec(P["q"], P["k"], P["v"], P["beta"], None, _hip.ptr(o),
-                                         _hip.ptr(hf), B, H, T, C, DK, DV, code, scale, ws.handle,
-                                         sh)
+                                         _hip.ptr(hf), B, H, T, C, DK, DV, code, ws.handle, sh)
         if st:
             _hip.check("pf_gdn_scan_output_exec", st)
         if ev is not None:

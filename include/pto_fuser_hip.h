@@ -61,18 +61,19 @@ void pf_gdn_teardown(void* ws);
 
 /* The two stages pf_gdn_exec enqueues, exposed so a caller can time or overlap them
  * separately.  Stage 1 (chunk-local, one workgroup per chunk) writes the within-chunk gate
- * cumsum G, T = (I + A)^-1 and the gated causal score P into the workspace — the work of the
- * reference's kkt_gated_native_v2 + tri_inv_rec_unroll + gated_qk nodes (fused.py:482-517,
- * registry.py:107-127).  Stage 2 (scan + output, state register-resident) reads them and
- * writes o and h_final — the reference's WY einsums, chunk_h_scan and qkv_flash_native_v2
- * (_gdn_full.py:199-233, scan_lib.cpp:81-99, qkv_fused_lib.cpp:148-165).  Stage 2 must be
- * ordered after stage 1 on the same workspace (same stream, or an event). */
+ * cumsum G, T = (I + A)^-1 and the gated causal score P (multiplied by `scale`) into the
+ * workspace, and records `scale` there — the work of the reference's kkt_gated_native_v2 +
+ * tri_inv_rec_unroll + gated_qk nodes (fused.py:482-517, registry.py:107-127).  Stage 2 (scan +
+ * output, state register-resident) reads them, the scale included, and writes o and h_final —
+ * the reference's WY einsums, chunk_h_scan and qkv_flash_native_v2 (_gdn_full.py:199-233,
+ * scan_lib.cpp:81-99, qkv_fused_lib.cpp:148-165).  Stage 2 must be ordered after stage 1 on the
+ * same workspace (same stream, or an event). */
 int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, const float* g,
-                            int B, int H, int T, int C, int DK, int DV, int dtype, void* ws,
-                            void* stream);
+                            int B, int H, int T, int C, int DK, int DV, int dtype, float scale,
+                            void* ws, void* stream);
 int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const float* beta,
                             const float* h0, float* o, float* h_final, int B, int H, int T, int C,
-                            int DK, int DV, int dtype, float scale, void* ws, void* stream);
+                            int DK, int DV, int dtype, void* ws, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Standalone kkt + triangular inverse over M independent chunks.

@@ -14,6 +14,10 @@
 #ifndef PF_TR_LOADER_WAVES
 #define PF_TR_LOADER_WAVES 4
 #endif
+// compute waves of the bf16 scan kernel; each owns 2 / PF_TR_COMPUTE_WAVES blocks of 16 columns
+#ifndef PF_TR_COMPUTE_WAVES
+#define PF_TR_COMPUTE_WAVES 2
+#endif
 
 namespace {
 
@@ -30,15 +34,17 @@ size_t elem_size(int dtype) { return dtype == PF_DTYPE_BF16 ? 2 : 4; }
 
 bool valid_dtype(int dtype) { return dtype == PF_DTYPE_F32 || dtype == PF_DTYPE_BF16; }
 
-// Byte layout of the fused-forward workspace: [ T (M*C*C E) | P (M*C*C E) | G (M*C fp32) ].
+// Byte layout of the fused-forward workspace:
+//   [ T (M*C*C E) | P (M*C*C E, pre-scaled) | G (M*C fp32) | output scale (fp32, 256 B slot) ].
 struct GdnLayout {
-  size_t t_off, p_off, g_off, total;
+  size_t t_off, p_off, g_off, s_off, total;
   GdnLayout(size_t M, int C, int dtype) {
     const size_t cc = M * C * C * elem_size(dtype);
     t_off = 0;
     p_off = align256(cc);
     g_off = p_off + align256(cc);
-    total = g_off + align256(M * C * sizeof(float));
+    s_off = g_off + align256(M * C * sizeof(float));
+    total = s_off + 256;
   }
 };
 
@@ -54,7 +60,7 @@ int launch_status() {
 
 template <typename E>
 int chunk_local_launch(const void* q, const void* k, const float* beta, const float* g,
-                       const GdnWorkspace* ws, size_t M, hipStream_t stream) {
+                       float scale, const GdnWorkspace* ws, size_t M, hipStream_t stream) {
   constexpr int C = 64, DK = 128;
   const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
   char* base = static_cast<char*>(ws->base);
@@ -70,13 +76,15 @@ int chunk_local_launch(const void* q, const void* k, const float* beta, const fl
   a.M = static_cast<int>(M);
   a.epi_mode = 0;
   a.g_is_cumsum = 0;
+  a.p_scale = scale;
+  a.scale_out = reinterpret_cast<float*>(base + lay.s_off);
   pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
   return launch_status();
 }
 
 template <typename E>
 int scan_output_launch(const void* q, const void* k, const void* v, const float* beta,
-                       const float* h0, float* o, float* h_final, int BH, int NC, float scale,
+                       const float* h0, float* o, float* h_final, int BH, int NC,
                        const GdnWorkspace* ws, hipStream_t stream) {
   constexpr int C = 64, DK = 128, DV = 128, NWC = 2;
   const size_t M = (size_t)BH * NC;
@@ -95,12 +103,13 @@ int scan_output_launch(const void* q, const void* k, const void* v, const float*
   a.h_final = h_final;
   a.BH = BH;
   a.NC = NC;
-  a.scale = scale;
+  a.scale = reinterpret_cast<const float*>(base + lay.s_off);
   const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
   if constexpr (std::is_same<E, bf16>::value) {
     // bf16: row-major staging read back through LDS transpose loads (gfx950)
-    constexpr int NLW = PF_TR_LOADER_WAVES;
-    pf::scan_output_tr_kernel<C, DK, DV, NWC, NLW><<<dim3(grid), dim3(64 * (NWC + NLW)), 0, stream>>>(a);
+    constexpr int NLW = PF_TR_LOADER_WAVES, NWT = PF_TR_COMPUTE_WAVES, NCB = 2 / NWT;
+    static_assert(NWT * NCB == 2, "the bf16 scan kernel covers 32 state columns per workgroup");
+    pf::scan_output_tr_kernel<C, DK, DV, NWT, NLW, NCB><<<dim3(grid), dim3(64 * (NWT + NLW)), 0, stream>>>(a);
   } else {
     // fp32: transposed tiles staged by the loader; one LDS buffer (the images are 143 KB)
     pf::scan_output_kernel<E, C, DK, DV, NWC, 1>
@@ -162,29 +171,29 @@ void pf_gdn_teardown(void* ws) {
 }
 
 int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, const float* g,
-                            int B, int H, int T, int C, int DK, int DV, int dtype, void* ws,
-                            void* stream) {
+                            int B, int H, int T, int C, int DK, int DV, int dtype, float scale,
+                            void* ws, void* stream) {
   const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
   if (st != PF_OK) return st;
   if (!q || !k || !beta) return PF_ERR_ARG;
   const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
   const size_t M = (size_t)B * H * (T / C);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PF_DTYPE_BF16) return chunk_local_launch<bf16>(q, k, beta, g, w, M, s);
-  return chunk_local_launch<float>(q, k, beta, g, w, M, s);
+  if (dtype == PF_DTYPE_BF16) return chunk_local_launch<bf16>(q, k, beta, g, scale, w, M, s);
+  return chunk_local_launch<float>(q, k, beta, g, scale, w, M, s);
 }
 
 int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const float* beta,
                             const float* h0, float* o, float* h_final, int B, int H, int T, int C,
-                            int DK, int DV, int dtype, float scale, void* ws, void* stream) {
+                            int DK, int DV, int dtype, void* ws, void* stream) {
   const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
   if (st != PF_OK) return st;
   if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
   const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PF_DTYPE_BF16)
-    return scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, scale, w, s);
-  return scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, scale, w, s);
+    return scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
+  return scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
 }
 
 int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
@@ -194,10 +203,11 @@ int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, 
     const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
     return st != PF_OK ? st : PF_ERR_ARG;
   }
-  const int st = pf_gdn_chunk_local_exec(q, k, beta, g, B, H, T, C, DK, DV, dtype, ws, stream);
+  const int st = pf_gdn_chunk_local_exec(q, k, beta, g, B, H, T, C, DK, DV, dtype, scale, ws,
+                                         stream);
   if (st != PF_OK) return st;
-  return pf_gdn_scan_output_exec(q, k, v, beta, h0, o, h_final, B, H, T, C, DK, DV, dtype, scale,
-                                 ws, stream);
+  return pf_gdn_scan_output_exec(q, k, v, beta, h0, o, h_final, B, H, T, C, DK, DV, dtype, ws,
+                                 stream);
 }
 
 int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_out, float* T_out,
@@ -216,6 +226,8 @@ int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_o
   a.M = M;
   a.epi_mode = 0;
   a.g_is_cumsum = g_is_cumsum ? 1 : 0;
+  a.p_scale = 1.f;
+  a.scale_out = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PF_DTYPE_BF16)
     pf::chunk_local_kernel<bf16, float, 64, 128, false, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(a);

@@ -5,7 +5,8 @@
 //   A     = strictly_lower( beta_i * safe_exp(G_i - G_j) * (k_i . k_j) )  (_gdn_full.py:73-75)
 //           [epi_mode 1: exp(min(G_i + log beta_i - G_j, 0)), kkt_fused.h:154-185]
 //   T     = (I + A)^-1                                                 (_gdn_full.py:76-78)
-//   P     = causal_incl_diag( (q_i . k_j) * exp(min(G_i - G_j, 0)) )   (_gdn_full.py:91-95)
+//   P     = p_scale * causal_incl_diag( (q_i . k_j) * exp(min(G_i - G_j, 0)) )
+//           (_gdn_full.py:91-95; the output scale of :97 is applied here, once per score element)
 //
 // Mapping on CDNA4: k and q chunk tiles are staged in LDS (row pitch padded by 16 bytes so the
 // MFMA operand reads are bank-conflict free per half wave); the 2*NB(NB+1)/2 lower-triangular
@@ -34,6 +35,8 @@ struct ChunkLocalArgs {
   int M;                // number of chunks
   int epi_mode;         // 0: beta_i*safe_exp(G_i-G_j)   1: exp(min(G_i+log beta_i-G_j, 0))
   int g_is_cumsum;      // 1: g already holds within-chunk cumulative sums
+  float p_scale;        // multiplies P (the forward's output scale)
+  float* scale_out;     // if set, block 0 records p_scale here for the scan stage
 };
 
 // (I + A)^-1 of one strictly-lower C x C block held in LDS (As, fp32, pitch C+4) into Ts (same
@@ -112,6 +115,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   const int m = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const size_t row0 = (size_t)m * C;
+  if (a.scale_out && m == 0 && tid == 0) *a.scale_out = a.p_scale;
 
   // ---- 1. stage k (and q), gates: every load issued before the first LDS store ----------------
   {
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
         else coef = __expf(fminf(gi + __logf(Bs[i]) - gj, 0.f));
         As[i * CP + j] = (i > j) ? coef * acc[ii] : 0.f;
       } else {
-        const float val = (i >= j) ? acc[ii] * __expf(fminf(gi - gj, 0.f)) : 0.f;
+        const float val = (i >= j) ? a.p_scale * acc[ii] * __expf(fminf(gi - gj, 0.f)) : 0.f;
         static_cast<E*>(a.P_out)[(size_t)m * C * C + i * C + j] = from_f32<E>(val);
       }
     }

@@ -9,7 +9,7 @@
 //   QS    = q_c S
 //   r     = beta (v - e^G * Y)
 //   v_new = T_c r          ( = U - W S  with W = T beta k e^G, U = T beta v; _gdn_full.py:79-84)
-//   o_c   = scale * (e^G * QS + P_c v_new)                              (_gdn_full.py:88-97)
+//   o_c   = scale * e^G * QS + P_c v_new   (P carries the scale from K1)  (_gdn_full.py:88-97)
 //   S     = e^{G_last} S + k_c^T (v_new * e^{G_last - G})               (_gdn_full.py:86-87)
 //
 // T_c = (I+A)^-1, P_c (gated causal score) and G (within-chunk cumsum) come from K1.  Every
@@ -41,7 +41,7 @@ struct ScanOutArgs {
   float* h_final;       // [BH, DK, DV] or null
   int BH;
   int NC;               // chunks per chain
-  float scale;
+  const float* scale;   // device scalar: the output scale K1 applied to P (written by K1)
 };
 
 constexpr int kLoaderWaves = 2;
@@ -59,7 +59,8 @@ struct ChunkStage {
   E ps[C * TP];
   E vts[TW * TP];
   float Bs[C];    // beta
-  float EG[C];    // e^{G_t}
+  float BEG[C];   // beta e^{G_t}
+  float EG[C];    // scale e^{G_t}
   float EL[C];    // e^{G_last - G_t}
   float DL[4];    // [0] = e^{G_last}
 };
@@ -134,6 +135,7 @@ __device__ __forceinline__ void put_row16(E* tile, int row, int col, int pitch, 
 template <typename E, int C, int DK, int DV, int NWC, int NBUF>
 __global__ __launch_bounds__(64 * (NWC + kLoaderWaves)) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void scan_output_kernel(ScanOutArgs a) {
+  const float oscale = *a.scale;
   constexpr int TW = 16 * NWC;
   using Stage = ChunkStage<E, C, DK, TW>;
   using Regs = ChunkRegs<E, C, DK, TW>;
@@ -256,7 +258,8 @@ void scan_output_kernel(ScanOutArgs a) {
     const float gl = __shfl(r.g, C - 1);
     if (ltid < C) {
       s.Bs[ltid] = r.b;
-      s.EG[ltid] = __expf(r.g);
+      s.BEG[ltid] = r.b * __expf(r.g);
+      s.EG[ltid] = oscale * __expf(r.g);
       s.EL[ltid] = __expf(gl - r.g);
       if (ltid == 0) s.DL[0] = __expf(gl);
     }
@@ -279,14 +282,14 @@ void scan_output_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int t = 16 * mb + 4 * g + ii;
-        R[mb][ii] = s.Bs[t] * (vv[ii] - s.EG[t] * Y[mb][ii]);
+        R[mb][ii] = s.Bs[t] * vv[ii] - s.BEG[t] * Y[mb][ii];
       }
     }
     // v_new = T r (T lower triangular: K blocks up to the diagonal)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
       VN[mb] = chain<E, NKB_C, RowsSwz>(zero4(), s.ts, 16 * mb + c, TP, R, (16 * mb + 16 + KB - 1) / KB, g);
-    // o = scale (e^G QS + P v_new)
+    // o = scale e^G QS + P v_new   (P is pre-scaled)
     float* ocol = a.o + tok0 * DV + col;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -294,7 +297,7 @@ void scan_output_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int t = 16 * mb + 4 * g + ii;
-        ocol[(size_t)t * DV] = a.scale * (s.EG[t] * QS[mb][ii] + O[ii]);
+        ocol[(size_t)t * DV] = s.EG[t] * QS[mb][ii] + O[ii];
       }
     }
     // S = e^{G_last} S + k^T (v_new e^{G_last - G})

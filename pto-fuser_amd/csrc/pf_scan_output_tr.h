@@ -2,25 +2,38 @@
 // operands staged row-major only and read transposed through LDS transpose loads.
 //
 // Same mathematics and workgroup decomposition as the generic kernel (pf_scan_output.h): one
-// workgroup per (chain bh, 32-column dv tile), two compute waves (16 state columns each, state
-// register-resident in fp32) and two loader waves, two LDS chunk buffers, one barrier per chunk:
+// workgroup per (chain bh, 32-column dv tile), NWC compute waves (16*NCB state columns each, the
+// state register-resident in fp32) and NLW loader waves, two LDS chunk buffers, one barrier per
+// chunk.  Per chunk c, with v, beta, G, T and the pre-scaled P from K1:
 //
-//   Y = k S,  QS = q S,  r = beta (v - e^G Y),  v_new = T r,
-//   o = scale (e^G QS + P v_new),  S = e^{G_last} S + k^T (v_new e^{G_last - G}).
+//   Y = k S,  r = beta v - beta e^G Y,  v_new = T r,
+//   o = scale e^G (q S) + P v_new,  S <- e^{G_last} S + k^T (v_new e^{G_last - G}).
 //
-// What is specific to gfx950 and bf16:
+// Work moved off the compute waves (which bound the kernel: every chunk is a serial chain of
+// dependent MFMAs, and the waves stall between instructions, so instructions per chunk are the
+// currency):
+//   * the loader stages beta*v in fp32, already transposed to the accumulator layout, and the gate
+//     tables beta e^G, scale e^G, e^{G_last - G} (the exponentials once per row, not per lane);
+//   * the per-chunk decay e^{G_last} of the state is deferred: the compute waves hold
+//     S~ = S / f with a running factor f folded into the gate tables, and multiply the state only
+//     when the loader decides to renormalise (f below e^-60, or the last chunk, so the final state
+//     is exact) — 32 multiplies per chunk become a rare branch;
+//   * the output is produced transposed (o^T = v_new^T P^T + (S^T q^T) scale e^G, the same
+//     registers with the MFMA operands swapped), so each lane holds four consecutive output
+//     columns and stores them as one 16-byte vector.
+//
+// gfx950 specifics:
 //   * k^T, the A operand of the state update, is read straight out of the row-major k tile with
 //     ds_read_b64_tr_b16: within each 16-lane group, lane l receives element (l & 3) of the
 //     4-element words addressed by lanes 4j + (l >> 2), j = 0..3.  Lane (c, g) therefore
 //     addresses k[32kb + 4g + (c >> 2)][16r + 4(c & 3) .. +3] and receives
-//     k[32kb + 4g + j][16r + c], j = 0..3 — the permuted-K operand of the MFMA chain.  The v
-//     tile is read into the accumulator layout the same way.  No transposed copy is staged.
-//   * every tile is written by the loader as whole 16-byte row vectors and swizzled (Swz) so that
-//     the row writes, the MFMA operand reads and the transpose reads are all free of LDS bank
-//     conflicts; the loader's lane-to-row mapping makes the swizzle's half-swap bit a
-//     compile-time constant, so no data is shuffled;
+//     k[32kb + 4g + j][16r + c], j = 0..3 — the permuted-K operand of the MFMA chain.
+//   * every bf16 tile is written by the loader as whole 16-byte row vectors and swizzled (Swz) so
+//     that the row writes, the MFMA operand reads and the transpose reads are all free of LDS bank
+//     conflicts; the loader's lane-to-row mapping makes the swizzle's half-swap bit a compile-time
+//     constant, so no data is shuffled;
 //   * global traffic uses raw buffer loads/stores with a per-chain descriptor: the chunk advance
-//     is a scalar offset, the lane part a constant vector offset, rows a small immediate.
+//     is a scalar offset, the lane part a constant vector offset.
 #pragma once
 
 #include "pf_scan_output.h"
@@ -39,11 +52,38 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// A 16-byte row vector bound for a Swz<RS,1> tile slot whose 8-byte halves are swapped when
+// `swap` (a compile-time constant at every call): the halves are loaded straight into the swapped
+// register positions, so the LDS store is a plain, conflict-free 16-byte write with no register
+// shuffle (a shuffle would wait for the load to land, and split 8-byte stores conflict).
+#ifndef PF_TR_SWAP_MODE
+#define PF_TR_SWAP_MODE 2
+#endif
+__device__ __forceinline__ uint4 buf_load16_sw(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                               bool swap) {
+  if (!swap || PF_TR_SWAP_MODE != 0) return buf_load16(r, voff, soff);
+  const auto lo = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  const auto hi = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 8, soff, 0);
+  return make_uint4(hi[0], hi[1], lo[0], lo[1]);
+}
+
 // Transposed 8-byte LDS read (see the header comment); p is an LDS address.
 __device__ __forceinline__ bf16x4 lds_read_tr(const bf16* p) {
   const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) i16x4*)(const_cast<bf16*>(p)));
   return __builtin_bit_cast(bf16x4, v);
+}
+
+__device__ __forceinline__ void put16(bf16* dst, const uint4& x, bool swap) {
+  if (!swap || PF_TR_SWAP_MODE == 0) {
+    *reinterpret_cast<uint4*>(dst) = x;
+  } else if (PF_TR_SWAP_MODE == 1) {
+    *reinterpret_cast<uint2*>(dst + 4) = make_uint2(x.x, x.y);
+    __asm__ __volatile__("" ::: "memory");
+    *reinterpret_cast<uint2*>(dst) = make_uint2(x.z, x.w);
+  } else {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(x.z, x.w, x.x, x.y);
+  }
 }
 
 __device__ __forceinline__ bf16x8 cat8(const bf16x4& lo, const bf16x4& hi) {
@@ -59,39 +99,48 @@ __device__ __forceinline__ floatx4 mfma_bf16(const bf16x8& a, const bf16x8& b, c
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// LDS image of one chunk (bf16), C = 64, DK = 128, tile width TW = 32.
+// LDS image of one chunk, C = 64, DK = 128, tile width TW = 32.
 template <int C, int DK, int TW>
 struct TrStage {
   static constexpr int KP = DK + 16;   // k, q: Swz<2,3>
   static constexpr int TP = C + 8;     // T, P: Swz<3,1>
-  static constexpr int VP = TW + 16;   // v: unswizzled
+  static constexpr int BP = C + 4;     // beta v, fp32, transposed: [tile column][row], 4-row
+                                       // groups swizzled: group' = group ^ 2 (column >> 3)
   bf16 ks[C * KP];
   bf16 qs[C * KP];
   bf16 ts[C * TP];
   bf16 ps[C * TP];
-  bf16 vs[C * VP];
-  float Bs[C];
-  float EG[C];
-  float EL[C];
-  float DL[4];
+  float bv[TW * BP];
+  float BEG[C];   // beta_t e^{G_t} f_c
+  float EGS[C];   // scale e^{G_t} f_c
+  float EL[C];    // e^{G_last - G_t} / f_{c+1}
+  float DL[4];    // [0] factor for the state at this chunk's update, [1] nonzero: apply it
 };
 
 // Loader register image of one chunk; NLW loader waves share the tile (k, q: 1024 vectors;
-// T, P: 512; v: 256 — per thread NK, NT, NV).
+// T, P: 512; v: 256 — per thread NK, NTP, NV).
 template <int NLW>
 struct TrRegs {
   static constexpr int NK = 1024 / (64 * NLW), NTP = 512 / (64 * NLW), NV = 256 / (64 * NLW);
   uint4 k[NK], q[NK], t[NTP], p[NTP], v[NV];
+  float vb[NV];   // beta of each v row this lane stages
   float g, b;
 };
 
-template <int C, int DK, int DV, int NWC, int NLW>
+#ifndef PF_TR_LOADER_PRIO
+#define PF_TR_LOADER_PRIO 3
+#endif
+
+// Renormalisation threshold of the deferred state decay (log of the smallest factor kept).
+constexpr float kLogFactorFloor = -60.f;
+
+template <int C, int DK, int DV, int NWC, int NLW, int NCB>
 __global__ __launch_bounds__(64 * (NWC + NLW)) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void scan_output_tr_kernel(ScanOutArgs a) {
-  constexpr int TW = 16 * NWC;
+  constexpr int TW = 16 * NWC * NCB;
   using Stage = TrStage<C, DK, TW>;
   using Regs = TrRegs<NLW>;
-  constexpr int KP = Stage::KP, TP = Stage::TP, VP = Stage::VP;
+  constexpr int KP = Stage::KP, TP = Stage::TP, BP = Stage::BP;
   constexpr int NT = DV / TW;
   static_assert(C == 64 && DK == 128 && TW == 32 && (NLW == 2 || NLW == 4),
                 "tile shapes of the transpose-read kernel are fixed: C 64, DK 128, 32-column tile");
@@ -120,13 +169,18 @@ void scan_output_tr_kernel(ScanOutArgs a) {
   const __amdgpu_buffer_rsrc_t rt = make_rsrc(static_cast<const bf16*>(a.Tm) + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(static_cast<const bf16*>(a.P) + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.o + (size_t)bh * Tlen * DV, Tlen * DV * 4);
-  const float* Gc = a.G ? a.G + (size_t)bh * Tlen : nullptr;
+  const float* Gc = a.G + (size_t)bh * Tlen;          // always written by K1
   const float* Bc = a.beta + (size_t)bh * Tlen;
 
   if (w >= NWC) {
     // =========================== loader waves ===========================
-    // (the gate tables below are filled by loader threads lt < C, i.e. the first loader wave)
+    // (the gate tables are filled by loader threads lt < C, i.e. the first loader wave)
     const int lt = tid - 64 * NWC;                       // 0 .. 64*NLW-1
+#if PF_TR_LOADER_PRIO
+    // loader waves share SIMDs with the compute waves: let their few instructions go first
+    __builtin_amdgcn_s_setprio(PF_TR_LOADER_PRIO);
+#endif
+    const float oscale = *a.scale;
     // Row mappings: the lane part of each row index is fixed per thread, the vector index i
     // supplies the bits that decide the swizzle's half swap (so the swap is compile-time).
     // k / q (16 vectors per row): vec = lt & 15, a = lt >> 4;
@@ -148,178 +202,247 @@ void scan_output_tr_kernel(ScanOutArgs a) {
     const uint32_t tp_voff = (uint32_t)(trow_l * C + tvec * 8) * 2;
     const int tp_lds = trow_l * TP + 8 * tvec;
     auto trow_i = [](int i) -> int { return NLW == 2 ? ((i & 1) << 3) | (((i >> 1) & 1) << 5) : ((i & 1) << 3); };
-    // v (4 vectors per row of the tile): row = (lt >> 2) + (16*NLW) i, vec = lt & 3
+    // v (4 vectors per row of the tile): row = (lt >> 2) + (16*NLW) i, columns 8 vvec .. +7
     const int vrow_l = lt >> 2, vvec = lt & 3;
     const uint32_t v_voff = (uint32_t)(vrow_l * DV + col0 + vvec * 8) * 2;
-    const int v_lds = vrow_l * VP + vvec * 8;
+    float Lrun = 0.f;                                   // log of the state factor f_c
 
     auto load_chunk = [&](Regs& r, int ch) {
       const uint32_t kq_s = (uint32_t)ch * C * DK * 2;
 #pragma unroll
       for (int i = 0; i < Regs::NK; ++i) {
         const uint32_t rowi = krow_i(i);
-        r.k[i] = buf_load16(rk, kq_voff, kq_s + rowi * DK * 2);
-        r.q[i] = buf_load16(rq, kq_voff, kq_s + rowi * DK * 2);
+        r.k[i] = buf_load16_sw(rk, kq_voff, kq_s + rowi * DK * 2, (i & 1) != 0);   // Swz<2,3>: i0
+        r.q[i] = buf_load16_sw(rq, kq_voff, kq_s + rowi * DK * 2, (i & 1) != 0);
       }
       const uint32_t tp_s = (uint32_t)ch * C * C * 2;
 #pragma unroll
       for (int i = 0; i < Regs::NTP; ++i) {
         const uint32_t rowi = trow_i(i);
-        r.t[i] = buf_load16(rt, tp_voff, tp_s + rowi * C * 2);
-        r.p[i] = buf_load16(rp, tp_voff, tp_s + rowi * C * 2);
+        r.t[i] = buf_load16_sw(rt, tp_voff, tp_s + rowi * C * 2, (i & 1) != 0);    // Swz<3,1>: i0
+        r.p[i] = buf_load16_sw(rp, tp_voff, tp_s + rowi * C * 2, (i & 1) != 0);
       }
       const uint32_t v_s = (uint32_t)ch * C * DV * 2;
 #pragma unroll
-      for (int i = 0; i < Regs::NV; ++i) r.v[i] = buf_load16(rv, v_voff, v_s + (uint32_t)(16 * NLW * i) * DV * 2);
-      r.g = 0.f;
-      r.b = 0.f;
-      if (lt < C) {
-        r.g = Gc ? Gc[(size_t)ch * C + lt] : 0.f;
-        r.b = Bc[(size_t)ch * C + lt];
+      for (int i = 0; i < Regs::NV; ++i) {
+        r.v[i] = buf_load16(rv, v_voff, v_s + (uint32_t)(16 * NLW * i) * DV * 2);
+        r.vb[i] = Bc[(size_t)ch * C + vrow_l + 16 * NLW * i];
       }
+      // every lane loads (lanes past the first loader wave repeat its rows): no branch around a
+      // load, so the compiler's wait counts stay exact and two chunks stay in flight
+      r.g = Gc[(size_t)ch * C + (lt & (C - 1))];
+      r.b = Bc[(size_t)ch * C + (lt & (C - 1))];
     };
-    auto store_chunk = [&](Stage& s, const Regs& r) {
+    auto store_chunk = [&](Stage& s, const Regs& r, int ch) {
 #pragma unroll
-      for (int i = 0; i < Regs::NK; ++i) {
+      for (int i = 0; i < Regs::NK; ++i) {                // halves already in swizzled order
         const int rowi = krow_i(i);
-        const bool swap = (i & 1) != 0;                   // Swz<2,3> bit 0 = row bit 2 = i0
-        *reinterpret_cast<uint4*>(s.ks + kq_lds + rowi * KP) = swap_halves_if(r.k[i], swap);
-        *reinterpret_cast<uint4*>(s.qs + kq_lds + rowi * KP) = swap_halves_if(r.q[i], swap);
+        put16(s.ks + kq_lds + rowi * KP, r.k[i], (i & 1) != 0);
+        put16(s.qs + kq_lds + rowi * KP, r.q[i], (i & 1) != 0);
       }
 #pragma unroll
       for (int i = 0; i < Regs::NTP; ++i) {
         const int rowi = trow_i(i);
-        const bool swap = (i & 1) != 0;                   // Swz<3,1> bit 0 = row bit 3 = i0
-        *reinterpret_cast<uint4*>(s.ts + tp_lds + rowi * TP) = swap_halves_if(r.t[i], swap);
-        *reinterpret_cast<uint4*>(s.ps + tp_lds + rowi * TP) = swap_halves_if(r.p[i], swap);
+        put16(s.ts + tp_lds + rowi * TP, r.t[i], (i & 1) != 0);
+        put16(s.ps + tp_lds + rowi * TP, r.p[i], (i & 1) != 0);
       }
 #pragma unroll
-      for (int i = 0; i < Regs::NV; ++i) *reinterpret_cast<uint4*>(s.vs + v_lds + 16 * NLW * i * VP) = r.v[i];
-      const float gl = __shfl(r.g, C - 1);
-      if (lt < C) {
-        s.Bs[lt] = r.b;
-        s.EG[lt] = __expf(r.g);
-        s.EL[lt] = __expf(gl - r.g);
-        if (lt == 0) s.DL[0] = __expf(gl);
+      for (int i = 0; i < Regs::NV; ++i) {
+        const int row = vrow_l + 16 * NLW * i;
+        const bf16x8 x = __builtin_bit_cast(bf16x8, r.v[i]);
+        const int prow = (((row >> 2) ^ (2 * vvec)) << 2) | (row & 3);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s.bv[(vvec * 8 + e) * BP + prow] = (float)x[e] * r.vb[i];
       }
+      // gate tables with the deferred state factor f_c = e^{Lrun}
+      const float gl = __shfl(r.g, C - 1);                // G_last (log of the chunk decay)
+      const float Ln = Lrun + gl;                         // log(e^{G_last} f_c)
+      const bool renorm = Ln < kLogFactorFloor || ch == NC - 1;
+      const float Lnext = renorm ? 0.f : Ln;
+      if (lt < C) {
+        const float eg = __expf(r.g + Lrun);
+        s.BEG[lt] = r.b * eg;
+        s.EGS[lt] = oscale * eg;
+        s.EL[lt] = __expf(gl - r.g - Lnext);
+        if (lt == 0) {
+          s.DL[0] = __expf(Ln);
+          s.DL[1] = renorm ? 1.f : 0.f;
+        }
+      }
+      Lrun = Lnext;
     };
 
+    // Barrier k (k = 1 .. NC) follows the compute of chunk k-1; before it the loader has stored
+    // chunk k into buffer k & 1.  Two chunks stay in flight in registers (ra, rb); the loop body
+    // is straight-line with one back edge (a mid-loop exit makes the compiler's wait counts
+    // conservative and collapses the pipeline); past the end the loads repeat the last chunk.
+    const int last = NC - 1;
     Regs ra, rb;
     load_chunk(ra, 0);
-    store_chunk(st[0], ra);
-    if (NC > 1) load_chunk(rb, 1);
-    if (NC > 2) load_chunk(ra, 2);
+    store_chunk(st[0], ra, 0);
+    load_chunk(rb, min(1, last));
+    load_chunk(ra, min(2, last));
     lds_barrier();
-    for (int ch = 0; ch < NC; ch += 2) {
-      if (ch + 1 < NC) {
-        store_chunk(st[1], rb);
-        if (ch + 3 < NC) load_chunk(rb, ch + 3);
-      }
+    int k = 1;
+    for (; k + 1 < NC; k += 2) {
+      store_chunk(st[1], rb, k);
+      load_chunk(rb, min(k + 2, last));
       lds_barrier();
-      if (ch + 1 >= NC) break;
-      if (ch + 2 < NC) {
-        store_chunk(st[0], ra);
-        if (ch + 4 < NC) load_chunk(ra, ch + 4);
-      }
+      store_chunk(st[0], ra, k + 1);
+      load_chunk(ra, min(k + 3, last));
       lds_barrier();
     }
+    if (k < NC) {                                        // k = NC - 1, odd
+      store_chunk(st[1], rb, k);
+      lds_barrier();
+    }
+    lds_barrier();                                       // barrier NC
   } else {
     // =========================== compute waves ===========================
-    const int col = col0 + w * 16 + c;
+    // Wave w owns NCB blocks of 16 state columns; every LDS A operand it reads (k, q, T, P, k^T)
+    // feeds the NCB blocks' MFMAs.
+    const int cbase = w * 16 * NCB;                      // first tile column of this wave
+    const int colw = col0 + cbase + c;                   // column of block cb: colw + 16 cb
     // per-lane LDS element offsets (see the swizzle derivations in the header comment)
-    const int kq_rd = c * KP + 4 * (g ^ ((c >> 2) & 3));             // A of k S / q S
+    const int kq_rd = c * KP + 4 * (g ^ ((c >> 2) & 3));             // k / q rows, permuted K
     const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g);   // transposed A of k^T
-    const int tp_rd = c * TP + 4 * (g ^ (c >> 3));                   // A of T r / P v_new
-    const int v_rd = (4 * g + (c >> 2)) * VP + 16 * w + 4 * (c & 3); // v rows 4g.. of col c
-    const uint32_t o_voff = (uint32_t)(4 * g * DV + col) * 4;
+    const int tp_rd = c * TP + 4 * (g ^ (c >> 3));                   // T / P rows, permuted K
+    const int bv_col = cbase + c;                                    // beta v column (tile)
+    // transposed output: lane holds token 16 mb + c, columns 4g .. 4g+3 of its 16-column block
+    const uint32_t o_voff = (uint32_t)(c * DV + col0 + cbase + 4 * g) * 4;
 
-    floatx4 S[DK / 16];
+    floatx4 S[NCB][DK / 16];
 #pragma unroll
-    for (int r = 0; r < DK / 16; ++r) {
+    for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii)
-        S[r][ii] = a.h0 ? a.h0[((size_t)bh * DK + 16 * r + 4 * g + ii) * DV + col] : 0.f;
-    }
+      for (int r = 0; r < DK / 16; ++r)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          S[cb][r][ii] = a.h0 ? a.h0[((size_t)bh * DK + 16 * r + 4 * g + ii) * DV + colw + 16 * cb] : 0.f;
 
     auto compute_chunk = [&](const Stage& s, int ch) {
-      // bf16 B operands of the state, one per 32-row K block
-      bf16x8 SB[DK / 32];
+      // bf16 state, one per 32-row K block: the B operand of k S and the A operand of S^T q^T
+      bf16x8 SB[NCB][DK / 32];
 #pragma unroll
-      for (int kb = 0; kb < DK / 32; ++kb) SB[kb] = pack8(S[2 * kb], S[2 * kb + 1]);
-      floatx4 Y[4], QS[4], R[4], VN[4];
+      for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        Y[mb] = zero4();
-        QS[mb] = zero4();
-      }
+        for (int kb = 0; kb < DK / 32; ++kb) SB[cb][kb] = pack8(S[cb][2 * kb], S[cb][2 * kb + 1]);
+      floatx4 Y[NCB][4], QT[NCB][4], R[NCB][4], VN[NCB][4];
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          Y[cb][mb] = zero4();
+          QT[cb][mb] = zero4();
+        }
 #pragma unroll
       for (int kb = 0; kb < DK / 32; ++kb) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
           const bf16* kp = s.ks + kq_rd + 16 * mb * KP + 32 * kb;
           const bf16* qp = s.qs + kq_rd + 16 * mb * KP + 32 * kb;
-          Y[mb] = mfma_bf16(cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16)),
-                            SB[kb], Y[mb]);
-          QS[mb] = mfma_bf16(cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16)),
-                             SB[kb], QS[mb]);
+          const bf16x8 ka = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
+          const bf16x8 qa = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb) {
+            Y[cb][mb] = mfma_bf16(ka, SB[cb][kb], Y[cb][mb]);      // (k S)[t][n]
+            QT[cb][mb] = mfma_bf16(SB[cb][kb], qa, QT[cb][mb]);    // (q S)^T[n][t]
+          }
         }
       }
-      // r = beta (v - e^G Y)
+      // r = beta v - beta e^G f Y~
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        const bf16x4 vv = lds_read_tr(s.vs + v_rd + 16 * mb * VP);
+        const floatx4 beg = *reinterpret_cast<const floatx4*>(s.BEG + 16 * mb + 4 * g);
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int t = 16 * mb + 4 * g + ii;
-          R[mb][ii] = s.Bs[t] * ((float)vv[ii] - s.EG[t] * Y[mb][ii]);
+        for (int cb = 0; cb < NCB; ++cb) {
+          const int n = bv_col + 16 * cb;
+          const floatx4 bvv = *reinterpret_cast<const floatx4*>(s.bv + n * BP + 4 * ((4 * mb + g) ^ (2 * (n >> 3))));
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) R[cb][mb][ii] = fmaf(-beg[ii], Y[cb][mb][ii], bvv[ii]);
         }
       }
       // v_new = T r (lower triangular: K block 1 only for rows 32..63)
-      const bf16x8 RB0 = pack8(R[0], R[1]), RB1 = pack8(R[2], R[3]);
+      bf16x8 RB0[NCB], RB1[NCB];
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        RB0[cb] = pack8(R[cb][0], R[cb][1]);
+        RB1[cb] = pack8(R[cb][2], R[cb][3]);
+      }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const bf16* tp = s.ts + tp_rd + 16 * mb * TP;
-        VN[mb] = mfma_bf16(cat8(*reinterpret_cast<const bf16x4*>(tp), *reinterpret_cast<const bf16x4*>(tp + 16)),
-                           RB0, zero4());
-        if (mb >= 2)
-          VN[mb] = mfma_bf16(cat8(*reinterpret_cast<const bf16x4*>(tp + 32), *reinterpret_cast<const bf16x4*>(tp + 48)),
-                             RB1, VN[mb]);
+        const bf16x8 t0 = cat8(*reinterpret_cast<const bf16x4*>(tp), *reinterpret_cast<const bf16x4*>(tp + 16));
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) VN[cb][mb] = mfma_bf16(t0, RB0[cb], zero4());
+        if (mb >= 2) {
+          const bf16x8 t1 = cat8(*reinterpret_cast<const bf16x4*>(tp + 32), *reinterpret_cast<const bf16x4*>(tp + 48));
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb) VN[cb][mb] = mfma_bf16(t1, RB1[cb], VN[cb][mb]);
+        }
       }
-      // o = scale (e^G QS + P v_new)
-      const bf16x8 VB0 = pack8(VN[0], VN[1]), VB1 = pack8(VN[2], VN[3]);
+      // o^T = v_new^T P^T + (scale e^G f) (S~^T q^T): v_new is the A operand as it stands
+      bf16x8 VB0[NCB], VB1[NCB];
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        VB0[cb] = pack8(VN[cb][0], VN[cb][1]);
+        VB1[cb] = pack8(VN[cb][2], VN[cb][3]);
+      }
       const uint32_t o_s = (uint32_t)ch * C * DV * 4;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const bf16* pp = s.ps + tp_rd + 16 * mb * TP;
-        floatx4 O = mfma_bf16(cat8(*reinterpret_cast<const bf16x4*>(pp), *reinterpret_cast<const bf16x4*>(pp + 16)),
-                              VB0, zero4());
-        if (mb >= 2)
-          O = mfma_bf16(cat8(*reinterpret_cast<const bf16x4*>(pp + 32), *reinterpret_cast<const bf16x4*>(pp + 48)),
-                        VB1, O);
+        const bf16x8 p0 = cat8(*reinterpret_cast<const bf16x4*>(pp), *reinterpret_cast<const bf16x4*>(pp + 16));
+        const float egs = s.EGS[16 * mb + c];
+        floatx4 OT[NCB];
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int t = 16 * mb + 4 * g + ii;
-          const float val = a.scale * (s.EG[t] * QS[mb][ii] + O[ii]);
-          // the builtin takes the 32 data bits as an unsigned int: pass the float's bits
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), ro, o_voff,
-                                                o_s + (uint32_t)(16 * mb + ii) * DV * 4, 0);
+        for (int cb = 0; cb < NCB; ++cb) OT[cb] = mfma_bf16(VB0[cb], p0, zero4());
+        if (mb >= 2) {
+          const bf16x8 p1 = cat8(*reinterpret_cast<const bf16x4*>(pp + 32), *reinterpret_cast<const bf16x4*>(pp + 48));
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb) OT[cb] = mfma_bf16(VB1[cb], p1, OT[cb]);
+        }
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+          floatx4 val;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) val[ii] = fmaf(egs, QT[cb][mb][ii], OT[cb][ii]);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, o_voff + 64 * cb,
+                                                 o_s + (uint32_t)(16 * mb) * DV * 4, 0);
         }
       }
-      // S = e^{G_last} S + k^T (v_new e^{G_last - G})
-      const float dl = s.DL[0];
+      // S~ <- (renormalise ? e^{G_last} f_c : 1) S~ + k^T (v_new e^{G_last - G} / f_{c+1})
+      bf16x8 UB0[NCB], UB1[NCB];
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
+        const floatx4 el = *reinterpret_cast<const floatx4*>(s.EL + 16 * mb + 4 * g);
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) VN[mb][ii] *= s.EL[16 * mb + 4 * g + ii];
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) VN[cb][mb][ii] *= el[ii];
       }
-      const bf16x8 UB0 = pack8(VN[0], VN[1]), UB1 = pack8(VN[2], VN[3]);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        UB0[cb] = pack8(VN[cb][0], VN[cb][1]);
+        UB1[cb] = pack8(VN[cb][2], VN[cb][3]);
+      }
+      if (s.DL[1] != 0.f) {
+        const float m = s.DL[0];
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+          for (int r = 0; r < DK / 16; ++r) S[cb][r] *= m;
+      }
 #pragma unroll
       for (int r = 0; r < DK / 16; ++r) {
         const bf16* k0 = s.ks + kt_rd + 16 * r;
-        floatx4 acc = S[r] * dl;
-        acc = mfma_bf16(cat8(lds_read_tr(k0), lds_read_tr(k0 + 16 * KP)), UB0, acc);
-        acc = mfma_bf16(cat8(lds_read_tr(k0 + 32 * KP), lds_read_tr(k0 + 48 * KP)), UB1, acc);
-        S[r] = acc;
+        const bf16x8 a0 = cat8(lds_read_tr(k0), lds_read_tr(k0 + 16 * KP));
+        const bf16x8 a1 = cat8(lds_read_tr(k0 + 32 * KP), lds_read_tr(k0 + 48 * KP));
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+          const floatx4 acc = mfma_bf16(a0, UB0[cb], S[cb][r]);
+          S[cb][r] = mfma_bf16(a1, UB1[cb], acc);
+        }
       }
     };
 
@@ -333,11 +456,12 @@ void scan_output_tr_kernel(ScanOutArgs a) {
     }
     if (a.h_final) {
 #pragma unroll
-      for (int r = 0; r < DK / 16; ++r) {
+      for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-          a.h_final[((size_t)bh * DK + 16 * r + 4 * g + ii) * DV + col] = S[r][ii];
-      }
+        for (int r = 0; r < DK / 16; ++r)
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii)
+            a.h_final[((size_t)bh * DK + 16 * r + 4 * g + ii) * DV + colw + 16 * cb] = S[cb][r][ii];
     }
   }
 }

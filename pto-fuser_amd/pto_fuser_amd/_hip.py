@@ -31,8 +31,8 @@ SIGNATURES = {
     "pf_gdn_setup": (c_void_p, [c_int] * 7),
     "pf_gdn_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
     "pf_gdn_teardown": (None, [c_void_p]),
-    "pf_gdn_chunk_local_exec": (c_int, [c_void_p] * 4 + [c_int] * 7 + [c_void_p, c_void_p]),
-    "pf_gdn_scan_output_exec": (c_int, [c_void_p] * 7 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
+    "pf_gdn_chunk_local_exec": (c_int, [c_void_p] * 4 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
+    "pf_gdn_scan_output_exec": (c_int, [c_void_p] * 7 + [c_int] * 7 + [c_void_p, c_void_p]),
     "pf_kkt_inv_exec": (c_int, [c_void_p] * 5 + [c_int] * 5 + [c_void_p]),
     "pf_tri_inv_exec": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "pf_gated_qk_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_void_p]),

@@ -59,9 +59,9 @@ def test_status_strings_and_version(lib):
 
 
 def test_workspace_sizing_contract(lib):
-    # T (bf16) + P (bf16) + G (fp32), each 256-byte aligned
+    # T (bf16) + P (bf16) + G (fp32), each 256-byte aligned, + a 256-byte slot for the scale
     M = 4 * 16 * 64
-    want = 2 * ((M * 64 * 64 * 2 + 255) // 256 * 256) + (M * 64 * 4 + 255) // 256 * 256
+    want = 2 * ((M * 64 * 64 * 2 + 255) // 256 * 256) + (M * 64 * 4 + 255) // 256 * 256 + 256
     assert lib.pf_gdn_workspace_bytes(4, 16, 4096, 64, 128, 128, _hip.PF_DTYPE_BF16) == want
     # unsupported shapes / dtypes report size 0 and setup refuses them
     assert lib.pf_gdn_workspace_bytes(1, 1, 100, 64, 128, 128, 1) == 0      # T % C != 0
@@ -84,9 +84,9 @@ def test_exec_rejects_contract_violations_before_launch(lib):
     assert lib.pf_tri_inv_exec(1, 1, 4, 96, None) == _hip.PF_ERR_ARG       # unsupported C
     assert lib.pf_kkt_inv_exec(None, None, None, None, None, 4, 64, 128, 1, 0, None) == _hip.PF_ERR_ARG
     assert lib.pf_gdn_chunk_local_exec(None, None, None, None, 1, 1, 128, 64, 128, 128, 1,
-                                       None, None) == _hip.PF_ERR_WORKSPACE
+                                       0.1, None, None) == _hip.PF_ERR_WORKSPACE
     assert lib.pf_gdn_scan_output_exec(None, None, None, None, None, None, None, 1, 1, 128, 64,
-                                       128, 128, 1, 0.1, None, None) == _hip.PF_ERR_WORKSPACE
+                                       128, 128, 1, None, None) == _hip.PF_ERR_WORKSPACE
     # stage kernels: null operands, unsupported (C, D, dtype) and bad output dtypes
     assert lib.pf_gated_qk_exec(None, None, None, None, None, None, None, None, 1, 1, 64, 128,
                                 1, 1, 0, None) == _hip.PF_ERR_ARG
