@@ -21,6 +21,9 @@
 
 #include "pf_device.h"
 
+// Barriers are LDS-only (lds_barrier): waves exchange data through LDS alone, so a barrier need
+// not wait for this wave's global stores to be acknowledged (a full __syncthreads would).
+
 namespace pf {
 
 struct ChunkLocalArgs {
@@ -63,7 +66,7 @@ __device__ __forceinline__ void block_unit_lower_inverse(const float* As, float*
 #pragma unroll
     for (int i = 0; i < 16; ++i) Ts[(16 * r + i) * CP + 16 * r + cc] = t[i];
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int L = 1; L < NB; ++L) {
     for (int j = w; j + L < NB; j += 4) {
@@ -83,7 +86,7 @@ __device__ __forceinline__ void block_unit_lower_inverse(const float* As, float*
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) Ts[(16 * i + 4 * g + ii) * CP + 16 * j + c] = -Y[ii];
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -107,7 +110,8 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
 
   __shared__ __attribute__((aligned(16))) char kqt[KQT_BYTES];
   __shared__ __attribute__((aligned(16))) float As[C * CP];
-  __shared__ float Gs[C], Bs[C];
+  __shared__ __attribute__((aligned(16))) float Gs[C];
+  __shared__ float Bs[C];
   E* ks = reinterpret_cast<E*>(kqt);
   E* qs = ks + C * KP;
   float* Ts = reinterpret_cast<float*>(kqt);
@@ -154,33 +158,60 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 2. gated score blocks: kkt (A) and, optionally, qk (P) -------------------------------
-  for (int x = w; x < NL * (DO_P ? 2 : 1); x += 4) {
-    const bool is_qk = x >= NL;
-    int idx = is_qk ? x - NL : x, bi = 0;
-    while (idx > bi) { idx -= bi + 1; ++bi; }
-    const int bj = idx;  // (bi, bj), bi >= bj
-    const E* arow = (is_qk ? qs : ks) + (16 * bi + c) * KP;
-    const E* brow = ks + (16 * bj + c) * KP;
-    floatx4 acc = zero4();
+  // Wave w owns the blocks x = w, w+4, ... of the list [kk blocks | qk blocks]; their MFMA chains
+  // are interleaved (independent accumulators), and each product is formed transposed —
+  // D[4g+ii][c] = sum_d b[j][d] a[i][d] with i = 16 bi + c, j = 16 bj + 4g + ii — so a lane holds
+  // four consecutive columns of one score row and stores them as one vector.
+  {
+    constexpr int NSB = NL * (DO_P ? 2 : 1), NPW = (NSB + 3) / 4;
+    floatx4 acc[NPW];
+    int bI[NPW], bJ[NPW];
+    bool isqk[NPW], valid[NPW];
 #pragma unroll
-    for (int kb = 0; kb < DK / Mfma<E>::KB; ++kb) acc = Mfma<E>::rows(acc, arow, brow, kb, g);
-    const int j = 16 * bj + c;
-    const float gj = Gs[j];
+    for (int sb = 0; sb < NPW; ++sb) {
+      const int x = w + 4 * sb;
+      valid[sb] = x < NSB;
+      isqk[sb] = x >= NL;
+      int idx = isqk[sb] ? x - NL : x, bi = 0;
+      while (idx > bi) { idx -= bi + 1; ++bi; }
+      bI[sb] = valid[sb] ? bi : 0;
+      bJ[sb] = valid[sb] ? idx : 0;
+      acc[sb] = zero4();
+    }
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int i = 16 * bi + 4 * g + ii;
+    for (int kb = 0; kb < DK / Mfma<E>::KB; ++kb) {
+#pragma unroll
+      for (int sb = 0; sb < NPW; ++sb) {
+        if (!valid[sb]) continue;
+        const E* jrow = ks + (16 * bJ[sb] + c) * KP;                    // k rows j
+        const E* irow = (isqk[sb] ? qs : ks) + (16 * bI[sb] + c) * KP;  // k or q rows i
+        acc[sb] = Mfma<E>::rows(acc[sb], jrow, irow, kb, g);
+      }
+    }
+#pragma unroll
+    for (int sb = 0; sb < NPW; ++sb) {
+      if (!valid[sb]) continue;
+      const int i = 16 * bI[sb] + c, j0 = 16 * bJ[sb] + 4 * g;
       const float gi = Gs[i];
-      if (!is_qk) {
-        float coef;
-        if (a.epi_mode == 0) coef = Bs[i] * safe_exp(gi - gj);
-        else coef = __expf(fminf(gi + __logf(Bs[i]) - gj, 0.f));
-        As[i * CP + j] = (i > j) ? coef * acc[ii] : 0.f;
+      const floatx4 gj = *reinterpret_cast<const floatx4*>(Gs + j0);
+      floatx4 out;
+      if (!isqk[sb]) {
+        const float bi = Bs[i];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const float coef = a.epi_mode == 0 ? bi * safe_exp(gi - gj[ii])
+                                             : __expf(fminf(gi + __logf(bi) - gj[ii], 0.f));
+          out[ii] = (i > j0 + ii) ? coef * acc[sb][ii] : 0.f;
+        }
+        *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
       } else {
-        const float val = (i >= j) ? a.p_scale * acc[ii] * __expf(fminf(gi - gj, 0.f)) : 0.f;
-        static_cast<E*>(a.P_out)[(size_t)m * C * C + i * C + j] = from_f32<E>(val);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          out[ii] = (i >= j0 + ii) ? a.p_scale * acc[sb][ii] * __expf(fminf(gi - gj[ii], 0.f)) : 0.f;
+        store4(static_cast<E*>(a.P_out) + (size_t)m * C * C + i * C + j0, out[0], out[1], out[2], out[3]);
       }
     }
   }
@@ -191,7 +222,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
       if ((j0 >> 4) > (i >> 4)) P[u] = make_uint4(0u, 0u, 0u, 0u);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   if (a.A_out) {
     float* Ao = a.A_out + (size_t)m * C * C;
@@ -232,7 +263,7 @@ __global__ __launch_bounds__(256) void tri_inv_kernel(const float* A, float* T, 
     const int i = e / C, j = e % C;
     As[i * CP + j] = (j < i) ? Ag[e] : 0.f;
   }
-  __syncthreads();
+  lds_barrier();
   block_unit_lower_inverse<C>(As, Ts);
   float* To = T + (size_t)m * C * C;
   for (int e = tid; e < C * C; e += 256) {

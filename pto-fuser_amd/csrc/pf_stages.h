@@ -24,6 +24,9 @@
 
 #include "pf_device.h"
 
+// Barriers are LDS-only (lds_barrier): waves exchange data through LDS alone, so a barrier need
+// not wait for this wave's global stores to be acknowledged (a full __syncthreads would).
+
 namespace pf {
 
 template <typename E> struct VecT;
@@ -92,7 +95,7 @@ __global__ __launch_bounds__(256) void gated_qk_kernel(GatedQkArgs p) {
     Gs[tid] = p.g ? p.g[gi] : 0.f;
     Ls[tid] = p.beta ? __logf(p.beta[gi]) : 0.f;
   }
-  __syncthreads();
+  lds_barrier();
   const size_t lrs = (size_t)p.H * C, lbase = ((size_t)ch * C * p.H + h) * C;
   for (int x = w; x < NB * NB; x += 4) {
     const int bi = x / NB, bj = x % NB, j = 16 * bj + c;
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(256) void qkv_flash_kernel(QkvFlashArgs p) {
     Gs[tid] = p.g ? p.g[row0 + tid] : 0.f;
     Ls[tid] = p.beta ? __logf(p.beta[row0 + tid]) : 0.f;
   }
-  __syncthreads();
+  lds_barrier();
   floatx4 acc[NPW];
 #pragma unroll
   for (int s = 0; s < NPW; ++s) {
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(256) void qkv_flash_kernel(QkvFlashArgs p) {
         acc[s] = Mfma<E>::rows(acc[s], rx + (16 * bi + c) * KP, ry + (16 * bj + c) * KP, kb, g);
     }
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int s = 0; s < NPW; ++s) {
     const int x = w + 4 * s;
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(256) void qkv_flash_kernel(QkvFlashArgs p) {
       for (int e = 0; e < VE; ++e) ry[(n0 + e) * VP + t] = x[e];
     }
   }
-  __syncthreads();
+  lds_barrier();
   // o[t, n] = sum_{t' <= t} S[t, t'] v[t', n]: (C/16) x (D/16) blocks over the four waves
   float* o = p.o + row0 * D;
   for (int x = w; x < NB * (D / 16); x += 4) {
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(64 * NW) void scan_state_kernel(ScanStateArgs p) {
     for (int i = tid; i < C * TW; i += NTHR) us[i] = ug[(i / TW) * rs + tile * TW + (i % TW)];
     for (int i = tid; i < D; i += NTHR)
       dec[i] = p.perdim ? p.decay[((size_t)bh * p.NC + ch) * D + i] : p.decay[(size_t)bh * p.NC + ch];
-    __syncthreads();
+    lds_barrier();
 
     // snapshot before the update
     const size_t hbase = (((size_t)b * p.NC + ch) * p.H + h) * D * D;
@@ -280,7 +283,7 @@ __global__ __launch_bounds__(64 * NW) void scan_state_kernel(ScanStateArgs p) {
       for (int ii = 0; ii < 4; ++ii) sd[ii] = S[r][ii] * dec[16 * r + 4 * g + ii];
       S[r] = chain<E, NKB_C, SW>(sd, kts, 16 * r + c, TP, Vc, NKB_C, g);
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (p.final_state) {
 #pragma unroll
