@@ -106,10 +106,15 @@ int scan_output_launch(const void* q, const void* k, const void* v, const float*
   a.scale = reinterpret_cast<const float*>(base + lay.s_off);
   const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
   if constexpr (std::is_same<E, bf16>::value) {
-    // bf16: row-major staging read back through LDS transpose loads (gfx950)
+    // bf16: row-major staging read back through LDS transpose loads (gfx950); its loader
+    // pipeline assumes at least two chunks per chain, a single chunk takes the generic kernel
     constexpr int NLW = PF_TR_LOADER_WAVES, NWT = PF_TR_COMPUTE_WAVES, NCB = 2 / NWT;
     static_assert(NWT * NCB == 2, "the bf16 scan kernel covers 32 state columns per workgroup");
-    pf::scan_output_tr_kernel<C, DK, DV, NWT, NLW, NCB><<<dim3(grid), dim3(64 * (NWT + NLW)), 0, stream>>>(a);
+    if (NC >= 2)
+      pf::scan_output_tr_kernel<C, DK, DV, NWT, NLW, NCB><<<dim3(grid), dim3(64 * (NWT + NLW)), 0, stream>>>(a);
+    else
+      pf::scan_output_kernel<E, C, DK, DV, NWC, 1>
+          <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
   } else {
     // fp32: transposed tiles staged by the loader; one LDS buffer (the images are 143 KB)
     pf::scan_output_kernel<E, C, DK, DV, NWC, 1>

@@ -146,6 +146,11 @@ void scan_output_tr_kernel(ScanOutArgs a) {
                 "tile shapes of the transpose-read kernel are fixed: C 64, DK 128, 32-column tile");
 
   __shared__ __attribute__((aligned(16))) Stage st[2];
+  // o of chunk c (fp32, [C][OP]) is staged in ost[c & 1] by the compute waves and written to HBM
+  // by the loader waves one interval later, so the compute waves never issue a vector-memory
+  // instruction (theirs would queue behind the loader's loads and stall the MFMA chain).
+  constexpr int OP = TW + 4;
+  __shared__ __attribute__((aligned(16))) float ost[2][C * OP];
 
   int bh, tile;
   const int bid = blockIdx.x;
@@ -272,31 +277,50 @@ void scan_output_tr_kernel(ScanOutArgs a) {
       Lrun = Lnext;
     };
 
-    // Barrier k (k = 1 .. NC) follows the compute of chunk k-1; before it the loader has stored
-    // chunk k into buffer k & 1.  Two chunks stay in flight in registers (ra, rb); the loop body
-    // is straight-line with one back edge (a mid-loop exit makes the compiler's wait counts
-    // conservative and collapses the pipeline); past the end the loads repeat the last chunk.
+    // o rows of a staged chunk: 8 16-byte vectors per row, two per loader thread
+    const int orow_l = lt >> 3, oseg = lt & 7;
+    const uint32_t o_voff = (uint32_t)(orow_l * DV + col0 + 4 * oseg) * 4;
+    auto store_o = [&](const float* os, int ch) {
+#pragma unroll
+      for (int i = 0; i < (C * TW / 4) / (64 * NLW); ++i) {
+        const int row = orow_l + (64 * NLW / 8) * i;
+        const floatx4 x = *reinterpret_cast<const floatx4*>(os + row * OP + 4 * oseg);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro, o_voff + (uint32_t)((64 * NLW / 8) * i * DV) * 4,
+                                               (uint32_t)ch * C * DV * 4, 0);
+      }
+    };
+
+    // Barrier j (j = 1 .. NC+1) follows the compute of chunk j-2.  Step j (between barriers j and
+    // j+1, j = 1 .. NC-1) first issues the loads of chunk j+2, then writes out the o of chunk
+    // j-2, then stores chunk j (loaded two steps earlier) into buffer j & 1.  Three register sets
+    // rotate, so a chunk's loads have two whole steps to land; the loop body is straight-line
+    // with one back edge (conditional code inside it makes the compiler's wait counts
+    // conservative); past the end the loads repeat the last chunk.
     const int last = NC - 1;
-    Regs ra, rb;
-    load_chunk(ra, 0);
-    store_chunk(st[0], ra, 0);
-    load_chunk(rb, min(1, last));
-    load_chunk(ra, min(2, last));
-    lds_barrier();
-    int k = 1;
-    for (; k + 1 < NC; k += 2) {
-      store_chunk(st[1], rb, k);
-      load_chunk(rb, min(k + 2, last));
+    Regs r0, r1, r2;
+    auto step = [&](Regs& ld, Regs& sd, int j, bool with_o) {
+      load_chunk(ld, min(j + 2, last));
+      if (with_o) store_o(ost[j & 1], j - 2);
+      store_chunk(st[j & 1], sd, j);
       lds_barrier();
-      store_chunk(st[0], ra, k + 1);
-      load_chunk(ra, min(k + 3, last));
-      lds_barrier();
+    };
+    load_chunk(r0, 0);
+    load_chunk(r1, min(1, last));
+    load_chunk(r2, min(2, last));
+    store_chunk(st[0], r0, 0);
+    lds_barrier();                                       // barrier 1
+    step(r0, r1, 1, false);                              // the host launches NC >= 2 only
+    int j = 2;
+    for (; j + 2 < NC; j += 3) {
+      step(r1, r2, j, true);
+      step(r2, r0, j + 1, true);
+      step(r0, r1, j + 2, true);
     }
-    if (k < NC) {                                        // k = NC - 1, odd
-      store_chunk(st[1], rb, k);
-      lds_barrier();
-    }
-    lds_barrier();                                       // barrier NC
+    if (j < NC) step(r1, r2, j, true);
+    if (j + 1 < NC) step(r2, r0, j + 1, true);
+    store_o(ost[NC & 1], NC - 2);
+    lds_barrier();                                       // barrier NC + 1
+    store_o(ost[(NC - 1) & 1], NC - 1);
   } else {
     // =========================== compute waves ===========================
     // Wave w owns NCB blocks of 16 state columns; every LDS A operand it reads (k, q, T, P, k^T)
@@ -309,7 +333,7 @@ void scan_output_tr_kernel(ScanOutArgs a) {
     const int tp_rd = c * TP + 4 * (g ^ (c >> 3));                   // T / P rows, permuted K
     const int bv_col = cbase + c;                                    // beta v column (tile)
     // transposed output: lane holds token 16 mb + c, columns 4g .. 4g+3 of its 16-column block
-    const uint32_t o_voff = (uint32_t)(c * DV + col0 + cbase + 4 * g) * 4;
+    const int o_lds = c * OP + cbase + 4 * g;
 
     floatx4 S[NCB][DK / 16];
 #pragma unroll
@@ -388,7 +412,7 @@ void scan_output_tr_kernel(ScanOutArgs a) {
         VB0[cb] = pack8(VN[cb][0], VN[cb][1]);
         VB1[cb] = pack8(VN[cb][2], VN[cb][3]);
       }
-      const uint32_t o_s = (uint32_t)ch * C * DV * 4;
+      float* os = ost[ch & 1];
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const bf16* pp = s.ps + tp_rd + 16 * mb * TP;
@@ -407,8 +431,7 @@ void scan_output_tr_kernel(ScanOutArgs a) {
           floatx4 val;
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) val[ii] = fmaf(egs, QT[cb][mb][ii], OT[cb][ii]);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, o_voff + 64 * cb,
-                                                 o_s + (uint32_t)(16 * mb) * DV * 4, 0);
+          *reinterpret_cast<floatx4*>(os + o_lds + 16 * mb * OP + 16 * cb) = val;
         }
       }
       // S~ <- (renormalise ? e^{G_last} f_c : 1) S~ + k^T (v_new e^{G_last - G} / f_{c+1})
