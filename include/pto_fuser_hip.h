@@ -76,6 +76,26 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
                             int DK, int DV, int dtype, void* ws, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Fused KDA forward (per-channel decay).  Replaces the lowered KDA program of
+ * examples/attention/_kda_full.py (host gate prep :78-103, the gated kkt / per-dim flash
+ * templates template.py:335-397 and the per-dim chunk_h_scan of transforms/kda.py:20-85 with
+ * scan_fused.h:143-180), the per-channel gate being applied on the device: stage 1 forms the
+ * gated operands k e^G, k e^-G, q e^G, k e^{G_last - G} from g, inverts (I + A) and builds the WY
+ * factors W, U and the score; stage 2 carries the state in registers with a per-channel decay.
+ * Math: kda_reference (_kda_full.py:42-76) plus an initial state h0 and the final state.
+ *   q, k [B,H,T,DK] bf16; v [B,H,T,DV] bf16; beta [B,H,T] fp32; g [B,H,T,DK] fp32 (per-token,
+ *   per-channel log decay, summed within each chunk of C tokens by the kernel); h0 [B,H,DK,DV]
+ *   fp32 or NULL; o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV] fp32 or NULL.
+ *   Supported: dtype PF_DTYPE_BF16, C = 64, DK = DV = 128, T % C == 0, T / C >= 2.
+ * ------------------------------------------------------------------------------------------ */
+size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
+void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype);
+int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
+                const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
+                int DV, int dtype, float scale, void* ws, void* stream);
+void pf_kda_teardown(void* ws);
+
+/* ------------------------------------------------------------------------------------------
  * Standalone kkt + triangular inverse over M independent chunks.
  * Replaces the kkt_gated_native FusedNode (fused.py:482-499, kkt_fused_lib.cpp:98-113)
  * followed by tri_inv_rec_unroll (registry.py:107-127):

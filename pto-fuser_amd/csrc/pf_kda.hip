@@ -1,0 +1,125 @@
+// extern "C" entry points of the fused KDA forward (declared in include/pto_fuser_hip.h).
+#include <hip/hip_runtime.h>
+
+#include <new>
+
+#include "../../include/pto_fuser_hip.h"
+#include "pf_kda.h"
+
+namespace {
+
+using pf::bf16;
+
+int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PF_OK : static_cast<int>(e);
+}
+
+constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct KdaWorkspace {
+  void* base = nullptr;
+  size_t bytes = 0;
+};
+
+// Byte layout of the KDA workspace, M = B*H*T/C chunks:
+//   [ W | U | QE | KR  (each M*C*128 bf16) | P (M*C*C bf16) | DEC (M*128 fp32) ]
+struct KdaLayout {
+  size_t w_off, u_off, q_off, k_off, p_off, d_off, total;
+  KdaLayout(size_t M, int C, int D) {
+    const size_t tile = align256(M * C * D * sizeof(bf16));
+    w_off = 0;
+    u_off = w_off + tile;
+    q_off = u_off + tile;
+    k_off = q_off + tile;
+    p_off = k_off + tile;
+    d_off = p_off + align256(M * C * C * sizeof(bf16));
+    total = d_off + align256(M * D * sizeof(float));
+  }
+};
+
+// bf16 operands, C = 64, dk = dv = 128, at least two chunks per chain (the scan kernel's loader
+// pipeline is written for NC >= 2).
+bool kda_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  return B > 0 && H > 0 && T > 0 && C == 64 && DK == 128 && DV == 128 && T % C == 0 &&
+         T / C >= 2 && dtype == PF_DTYPE_BF16;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  if (!kda_shape_ok(B, H, T, C, DK, DV, dtype)) return 0;
+  return KdaLayout((size_t)B * H * (T / C), C, DK).total;
+}
+
+void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  const size_t bytes = pf_kda_workspace_bytes(B, H, T, C, DK, DV, dtype);
+  if (bytes == 0) return nullptr;
+  KdaWorkspace* ws = new (std::nothrow) KdaWorkspace();
+  if (!ws) return nullptr;
+  if (hipMalloc(&ws->base, bytes) != hipSuccess) {
+    delete ws;
+    return nullptr;
+  }
+  ws->bytes = bytes;
+  return ws;
+}
+
+void pf_kda_teardown(void* ws) {
+  KdaWorkspace* w = static_cast<KdaWorkspace*>(ws);
+  if (!w) return;
+  if (w->base) (void)hipFree(w->base);
+  delete w;
+}
+
+int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
+                const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
+                int DV, int dtype, float scale, void* ws, void* stream) {
+  if (!kda_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
+  const KdaWorkspace* w = static_cast<const KdaWorkspace*>(ws);
+  const size_t M = (size_t)B * H * (T / C);
+  const KdaLayout lay(M, C, DK);
+  if (!w || !w->base || w->bytes < lay.total) return PF_ERR_WORKSPACE;
+  if (!q || !k || !v || !beta || !g || !o) return PF_ERR_ARG;
+  constexpr int KC = 64, KD = 128;
+  char* base = static_cast<char*>(w->base);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  pf::KdaLocalArgs la{};
+  la.q = static_cast<const bf16*>(q);
+  la.k = static_cast<const bf16*>(k);
+  la.v = static_cast<const bf16*>(v);
+  la.g = g;
+  la.beta = beta;
+  la.scale = scale;
+  la.W = reinterpret_cast<bf16*>(base + lay.w_off);
+  la.U = reinterpret_cast<bf16*>(base + lay.u_off);
+  la.QE = reinterpret_cast<bf16*>(base + lay.q_off);
+  la.KR = reinterpret_cast<bf16*>(base + lay.k_off);
+  la.P = reinterpret_cast<bf16*>(base + lay.p_off);
+  la.DEC = reinterpret_cast<float*>(base + lay.d_off);
+  pf::kda_local_kernel<KC, KD, KD><<<dim3((unsigned)M), dim3(256), 0, s>>>(la);
+  int st = launch_status();
+  if (st != PF_OK) return st;
+
+  pf::KdaScanArgs sa{};
+  sa.W = la.W;
+  sa.U = la.U;
+  sa.QE = la.QE;
+  sa.KR = la.KR;
+  sa.P = la.P;
+  sa.DEC = la.DEC;
+  sa.h0 = h0;
+  sa.o = o;
+  sa.h_final = h_final;
+  sa.BH = B * H;
+  sa.NC = T / C;
+  constexpr int NLW = 4;
+  const unsigned grid = (unsigned)(B * H * (KD / 32));
+  pf::kda_scan_kernel<KC, KD, KD, NLW><<<dim3(grid), dim3(64 * (2 + NLW)), 0, s>>>(sa);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -16,7 +16,7 @@ from .gate import GateResult, frob_rel, gate_determinism, gate_frob_rel, gate_ou
 from .graph import CaptureExecutor, GraphReplayExecutor
 from .ir import (EinsumNode, FusedNode, Node, OpaqueNode, Program, TensorOp, TensorRef,
                  VecGlueNode)
-from .ops import chunk_scan, gated_qk, gdn_chunk_forward, kkt_inverse, qkv_flash, tri_inv
+from .ops import chunk_scan, gated_qk, gdn_chunk_forward, kda_chunk_forward, kkt_inverse, qkv_flash, tri_inv
 from .policy import PlannedTransform, Policy
 from .registry import OpaqueContract, OpaqueRegistry, capture_mode, default_registry
 from .report import CompilationReport, TransformRecord
@@ -27,7 +27,7 @@ from .transform import (EnableDirectReads, EnableFusedStore, Transform, Transfor
                         canonicalize)
 
 __all__ = [
-    "gdn_chunk_forward", "kkt_inverse", "tri_inv", "gated_qk", "qkv_flash", "chunk_scan",
+    "gdn_chunk_forward", "kda_chunk_forward", "kkt_inverse", "tri_inv", "gated_qk", "qkv_flash", "chunk_scan",
     "TensorRef", "Node", "EinsumNode", "OpaqueNode", "VecGlueNode", "TensorOp", "FusedNode",
     "Program", "StagedExecutor", "library_modes", "OpaqueRegistry", "OpaqueContract",
     "default_registry", "capture_mode", "GateResult", "FusedContract", "FusedKernel",

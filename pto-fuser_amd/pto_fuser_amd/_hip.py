@@ -38,6 +38,10 @@ SIGNATURES = {
     "pf_gated_qk_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_void_p]),
     "pf_qkv_flash_exec": (c_int, [c_void_p] * 8 + [c_int] * 4 + [c_void_p]),
     "pf_scan_exec": (c_int, [c_void_p] * 7 + [c_int] * 8 + [c_void_p]),
+    "pf_kda_workspace_bytes": (c_size_t, [c_int] * 7),
+    "pf_kda_setup": (c_void_p, [c_int] * 7),
+    "pf_kda_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
+    "pf_kda_teardown": (None, [c_void_p]),
 }
 
 

@@ -3,6 +3,8 @@
 * :func:`gdn_chunk_forward` — the fused gated delta-rule chunked forward (GDN; DeltaNet when
   ``g is None``): o and the final state h.  Math of gdn_reference
   (examples/attention/_gdn_full.py:57-97) plus an initial state.
+* :func:`kda_chunk_forward` — the fused KDA forward (per-channel decay): o and the final state.
+  Math of kda_reference (examples/attention/_kda_full.py:42-76) plus an initial state.
 * :func:`kkt_inverse` — the standalone gated kkt + (I + A)^-1 stage (fused.py:482-499 followed
   by registry.py:107-127).
 * :func:`tri_inv` — the opaque unit-lower inverse (registry.py:107-127).
@@ -78,6 +80,37 @@ def gdn_workspace(B, H, T, C, DK, DV, dtype: torch.dtype, device) -> GdnWorkspac
     ws = _WORKSPACES.get(key)
     if ws is None:
         ws = GdnWorkspace(B, H, T, C, DK, DV, code, device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+class KdaWorkspace:
+    """Persistent per-shape workspace of the fused KDA forward (pf_kda_setup / pf_kda_teardown):
+    the gated operands, the WY factors, the score and the chunk decays between its two
+    kernels."""
+
+    def __init__(self, B, H, T, C, DK, DV, dtype_code, device) -> None:
+        lib = _hip.load()
+        with torch.cuda.device(device):
+            handle = lib.pf_kda_setup(B, H, T, C, DK, DV, dtype_code)
+        if not handle:
+            raise _hip.HipKernelError("pf_kda_setup", _hip.PF_ERR_ALLOC,
+                                      "workspace allocation failed or shape unsupported")
+        self.handle = handle
+        self.key = ("kda", B, H, T, C, DK, DV, dtype_code, str(device))
+        self.bytes = lib.pf_kda_workspace_bytes(B, H, T, C, DK, DV, dtype_code)
+        self._finalizer = weakref.finalize(self, lib.pf_kda_teardown, handle)
+
+    def close(self) -> None:
+        self._finalizer()
+
+
+def kda_workspace(B, H, T, C, DK, DV, dtype: torch.dtype, device) -> KdaWorkspace:
+    code = _dtype_code(dtype)
+    key = ("kda", B, H, T, C, DK, DV, code, str(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        ws = KdaWorkspace(B, H, T, C, DK, DV, code, device)
         _WORKSPACES[key] = ws
     return ws
 
@@ -312,3 +345,58 @@ def tri_inv(A: torch.Tensor) -> torch.Tensor:
                                      _hip.current_stream_handle(A.device))
     _hip.check("pf_tri_inv_exec", st)
     return out
+
+
+def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                      g: torch.Tensor, scale: Optional[float] = None,
+                      h0: Optional[torch.Tensor] = None, chunk_size: int = 64,
+                      output_final_state: bool = True,
+                      out: Optional[torch.Tensor] = None,
+                      final_out: Optional[torch.Tensor] = None,
+                      workspace: Optional[KdaWorkspace] = None,
+                      ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Fused chunked KDA forward (per-channel decay) on the current HIP stream.
+
+    q, k [B,H,T,DK] and v [B,H,T,DV] bfloat16; beta [B,H,T] float32; g [B,H,T,DK] float32 (the
+    per-token, per-channel log decay, summed within chunks by the kernel); h0 [B,H,DK,DV]
+    float32 or None.  Returns (o [B,H,T,DV] float32 scaled by ``scale`` (default DK^-1/2),
+    h_final [B,H,DK,DV] float32 or None).  At least two chunks per sequence (T >= 2 C); float32
+    operands are served by the staged KDA program (forwards.kda) instead."""
+    if q.dim() != 4:
+        raise ValueError(f"q must be [B,H,T,DK], got shape {tuple(q.shape)}")
+    B, H, T, DK = q.shape
+    DV = v.shape[-1]
+    C = int(chunk_size)
+    if C not in SUPPORTED_C or DK not in SUPPORTED_D or DV not in SUPPORTED_D:
+        raise ValueError(f"unsupported shape C={C} DK={DK} DV={DV} "
+                         f"(C in {SUPPORTED_C}, DK/DV in {SUPPORTED_D})")
+    if T % C or T // C < 2:
+        raise ValueError(f"T={T} must be a multiple of the chunk size {C} with at least two chunks")
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"the fused KDA forward takes bfloat16 operands, got {q.dtype}")
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError(f"q must be on a HIP device, got {dev}")
+    _require(q, "q", (B, H, T, DK), q.dtype, dev)
+    _require(k, "k", (B, H, T, DK), q.dtype, dev)
+    _require(v, "v", (B, H, T, DV), q.dtype, dev)
+    _require(beta, "beta", (B, H, T), torch.float32, dev)
+    if g is None:
+        raise ValueError("g (the per-channel log decay [B,H,T,DK]) is required")
+    _require(g, "g", (B, H, T, DK), torch.float32, dev)
+    _require(h0, "h0", (B, H, DK, DV), torch.float32, dev)
+    o = out if out is not None else torch.empty(B, H, T, DV, device=dev, dtype=torch.float32)
+    _require(o, "out", (B, H, T, DV), torch.float32, dev)
+    hf = None
+    if output_final_state:
+        hf = final_out if final_out is not None else torch.empty(B, H, DK, DV, device=dev,
+                                                                 dtype=torch.float32)
+        _require(hf, "final_out", (B, H, DK, DV), torch.float32, dev)
+    ws = workspace or kda_workspace(B, H, T, C, DK, DV, q.dtype, dev)
+    sc = float(DK ** -0.5 if scale is None else scale)
+    lib = _hip.load()
+    st = lib.pf_kda_exec(_hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(beta), _hip.ptr(g),
+                         _hip.ptr(h0), _hip.ptr(o), _hip.ptr(hf), B, H, T, C, DK, DV,
+                         _hip.PF_DTYPE_BF16, sc, ws.handle, _hip.current_stream_handle(dev))
+    _hip.check("pf_kda_exec", st)
+    return o, hf

@@ -71,6 +71,21 @@ def test_workspace_sizing_contract(lib):
     assert not lib.pf_gdn_setup(1, 1, 100, 64, 128, 128, 1)
 
 
+def test_kda_workspace_and_rejects(lib):
+    # W, U, QE, KR (bf16 [M,C,128] each) + P (bf16 [M,C,C]) + DEC (fp32 [M,128]), 256-B aligned
+    M = 2 * 32 * 128
+    want = 4 * ((M * 64 * 128 * 2 + 255) // 256 * 256) + (M * 64 * 64 * 2 + 255) // 256 * 256 \
+        + (M * 128 * 4 + 255) // 256 * 256
+    assert lib.pf_kda_workspace_bytes(2, 32, 8192, 64, 128, 128, _hip.PF_DTYPE_BF16) == want
+    assert lib.pf_kda_workspace_bytes(1, 1, 8192, 64, 128, 128, _hip.PF_DTYPE_F32) == 0   # bf16 only
+    assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_BF16) == 0    # one chunk
+    assert not lib.pf_kda_setup(1, 1, 100, 64, 128, 128, 1)
+    assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
+                           1, 0.1, None, None) == _hip.PF_ERR_WORKSPACE
+    assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
+                           0, 0.1, None, None) == _hip.PF_ERR_ARG
+
+
 def test_exec_rejects_contract_violations_before_launch(lib):
     """Bad shapes, null pointers and missing workspaces return negative codes; nothing is
     enqueued (the calls are safe without a device)."""
@@ -120,3 +135,12 @@ def test_ops_validate_on_host():
         tri_inv(torch.zeros(2, 64, 32))
     with pytest.raises(ValueError):
         kkt_inverse(torch.zeros(64, 128), None, torch.zeros(64), chunk_size=32)
+    from pto_fuser_amd import kda_chunk_forward
+    qb = torch.zeros(1, 1, 128, 128, dtype=torch.bfloat16)
+    gk = torch.zeros(1, 1, 128, 128)
+    with pytest.raises(ValueError, match="HIP device"):
+        kda_chunk_forward(qb, qb, qb, torch.zeros(1, 1, 128), gk)
+    with pytest.raises(ValueError, match="bfloat16"):
+        kda_chunk_forward(qb.float(), qb.float(), qb.float(), torch.zeros(1, 1, 128), gk)
+    with pytest.raises(ValueError, match="two chunks"):
+        kda_chunk_forward(qb[:, :, :64], qb[:, :, :64], qb[:, :, :64], torch.zeros(1, 1, 64), gk[:, :, :64])
