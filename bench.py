@@ -16,7 +16,9 @@ Besides the required fields the line carries:
   * ``stages`` — both kernels' average durations, algorithmic bytes and flops, and their
     HBM / MFMA fractions;
   * ``cpu_baseline`` — the CPU oracle (a restatement of the reference's per-(b,h,c) loop, fp32
-    numpy, one BLAS thread) timed on this host over the same seeded inputs.
+    numpy, one BLAS thread) timed on this host over the same seeded inputs;
+  * ``secondary`` — the fused KDA forward (per-channel decay) at its benchmark configuration
+    B=2, H=32, T=8192, timed the same way (not the headline; skipped with --no-secondary).
 """
 from __future__ import annotations
 
@@ -104,6 +106,58 @@ def cpu_baseline(inputs, runs: int = 3):
                        f"1 BLAS thread, median of {runs} runs ({', '.join(f'{s:.2f}' for s in times)} s)")}
 
 
+KDA_WORKLOAD = dict(B=2, H=32, T=8192, C=64, DK=128, DV=128)
+
+
+def kda_model(B, H, T, C, DK, DV):
+    """Algorithmic HBM bytes of the fused KDA forward per chunk of C tokens (bf16 operands):
+    stage 1 reads q, k, v (bf16), g (fp32 per channel), beta and writes W, U, QE, KR (bf16),
+    P (bf16), the chunk decay (fp32); stage 2 reads W, QE, KR, U, P, the decay and writes o
+    (fp32).  ``compulsory`` is what any forward must move: q, k, v, g, beta in, o out."""
+    M = B * H * (T // C)
+    s1 = 3 * C * DK * 2 + C * DK * 4 + C * 4 + 4 * C * DK * 2 + C * C * 2 + DK * 4
+    s2 = 4 * C * DK * 2 + C * C * 2 + DK * 4 + C * DV * 4
+    final = B * H * DK * DV * 4
+    compulsory = M * (3 * C * DK * 2 + C * DK * 4 + C * 4 + C * DV * 4) + final
+    return {"units": M, "bytes_per_unit": s1 + s2, "bytes": M * (s1 + s2) + final,
+            "compulsory_bytes": compulsory}
+
+
+def kda_secondary(steps: int, warmup: int):
+    """Fused KDA forward at KDA_WORKLOAD: events around each forward on the launch stream."""
+    import torch
+    from pto_fuser_amd.forwards import make_delta_inputs
+    from pto_fuser_amd.ops import kda_chunk_forward, kda_workspace
+    dev = torch.device("cuda:0")
+    B, H, T, C, DK, DV = (KDA_WORKLOAD[k] for k in ("B", "H", "T", "C", "DK", "DV"))
+    d = make_delta_inputs(B, H, T, DK, DV, kind="kda", dtype=torch.bfloat16, seed=5, device=dev)
+    o = torch.empty(B, H, T, DV, device=dev, dtype=torch.float32)
+    hf = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32)
+    ws = kda_workspace(B, H, T, C, DK, DV, torch.bfloat16, dev)
+    run = lambda: kda_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], out=o,  # noqa: E731
+                                    final_out=hf, workspace=ws)
+    for _ in range(warmup):
+        run()
+    stream = torch.cuda.current_stream(dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for e in evs:
+        e[0].record(stream)
+        run()
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    m = kda_model(B, H, T, C, DK, DV)
+    return {"workload": "KDA chunked forward B2 H32 T8192 C64 dk128 dv128, per-channel decay, "
+                        "bf16 in, fp32 state/accum/o", **KDA_WORKLOAD,
+            "ms_per_step": round(ms, 5), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "kernels": ["kda_local", "kda_scan"], "bytes": m["bytes"],
+            "bytes_per_unit": m["bytes_per_unit"], "units": m["units"],
+            "hbm_frac": round(m["bytes"] / (ms * 1e-3) / PEAK_HBM, 4),
+            "compulsory_bytes": m["compulsory_bytes"],
+            "compulsory_hbm_frac": round(m["compulsory_bytes"] / (ms * 1e-3) / PEAK_HBM, 4)}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,6 +165,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--no-secondary", action="store_true", help="skip the KDA secondary record")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run three plain device copies of MIB MiB: the "
                          "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -230,6 +285,8 @@ def main(argv=None) -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         line["calibration_copy_bytes"] = n * 4
+    if not args.no_secondary:
+        line["secondary"] = {"kda_config5": kda_secondary(args.steps, args.warmup)}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(inputs, runs=args.cpu_runs)
     print(json.dumps(line), flush=True)
