@@ -104,17 +104,18 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   constexpr int NVT = NV / 256;                     // per thread
   static_assert(NV % 256 == 0, "k/q chunk tile must divide over 256 threads");
   constexpr int KQ_BYTES = (DO_P ? 2 : 1) * C * KP * (int)sizeof(E);
-  constexpr int T_BYTES = DO_INV ? C * CP * 4 : 16;
-  // T is written only after the last score read of k/q (a barrier apart), so it reuses their LDS.
-  constexpr int KQT_BYTES = KQ_BYTES > T_BYTES ? KQ_BYTES : T_BYTES;
+  constexpr int AT_BYTES = (DO_INV ? 2 : 1) * C * CP * 4;
+  // A and T are written only after the last score read of k/q (a barrier apart), so they reuse
+  // the k/q tiles' LDS: 35 KB per workgroup for bf16, four workgroups per CU.
+  constexpr int KQT_BYTES = KQ_BYTES > AT_BYTES ? KQ_BYTES : AT_BYTES;
 
   __shared__ __attribute__((aligned(16))) char kqt[KQT_BYTES];
-  __shared__ __attribute__((aligned(16))) float As[C * CP];
   __shared__ __attribute__((aligned(16))) float Gs[C];
   __shared__ float Bs[C];
   E* ks = reinterpret_cast<E*>(kqt);
   E* qs = ks + C * KP;
-  float* Ts = reinterpret_cast<float*>(kqt);
+  float* As = reinterpret_cast<float*>(kqt);
+  float* Ts = As + C * CP;
 
   const int m = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
@@ -191,6 +192,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
         acc[sb] = Mfma<E>::rows(acc[sb], jrow, irow, kb, g);
       }
     }
+    lds_barrier();   // every wave is done reading k / q: A now overwrites them
 #pragma unroll
     for (int sb = 0; sb < NPW; ++sb) {
       if (!valid[sb]) continue;
