@@ -102,6 +102,15 @@ class CostModel:
             saved = _us(staged - fused, 10 * nc - 4)
             return Prediction(saved, f"S kept in registers: {nc} chunks x ~10 kernels and "
                                      f"{(staged - fused) / 1e6:.1f} MB of state traffic removed")
+        if transform_name in ("fuse-gdn-forward", "fuse-kda-forward"):
+            # staged: every stage through HBM (the kkt score, T, W/U, the per-chunk state and
+            # v_new, the chunk_o score) and ~10 kernels per chunk for the unrolled scan;
+            # fused: q, k, v, gates in, o out, plus the WY factors once through HBM.
+            staged = N * nc * (10 * D * D * e + 9 * C * D * e) + M * (6 * C * C * 4 + 8 * C * D * e)
+            fused = M * (3 * C * D * e + C * D * 4 + 4 * C * D * e + C * C * e)
+            saved = _us(max(staged - fused, 0), 10 * nc + 20)
+            return Prediction(saved, f"whole forward in 2 kernels: {(staged - fused) / 1e6:.1f} MB "
+                                     f"of stage traffic and ~{10 * nc + 20} launches removed")
         if transform_name == "batch-chunk-intra-score":
             saved = _us(2 * M * C * C * 4, 2 * (nc - 1))
             return Prediction(saved, f"{nc} per-chunk intra scores -> one launch over {M} chunks",

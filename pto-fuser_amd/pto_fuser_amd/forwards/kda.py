@@ -24,7 +24,7 @@ from ._builder import ProgramBuilder
 __all__ = ["make_kda_inputs", "prepare_kda_bindings", "build_kda_program", "KDA_PROGRAM_INPUTS"]
 
 KDA_PROGRAM_INPUTS = ["qF", "kF", "vF", "coef_ag", "coef_bg", "coef_beta", "coef_wg", "coef_ub",
-                      "coef_krest", "coef_S"]
+                      "coef_krest", "coef_S", "g_native", "beta_native"]
 
 
 def make_kda_inputs(B, H, nc, C, D, device="cpu", dtype=torch.bfloat16, seed: int = 0
@@ -44,7 +44,9 @@ def make_kda_inputs(B, H, nc, C, D, device="cpu", dtype=torch.bfloat16, seed: in
 
 def prepare_kda_bindings(q, k, v, beta, g_in, work=torch.bfloat16) -> Dict[str, torch.Tensor]:
     """Per-channel gate coefficients (_kda_full.py:78-103), computed in fp32, stored in
-    ``work``."""
+    ``work``.  ``g_native`` (the within-chunk cumulative log decay, [M, C, D]) and
+    ``beta_native`` ([M, C]) stay fp32: the staged program does not read them, the whole-forward
+    rewrite hands them to the fused KDA kernels."""
     B, H, nc, C, D = q.shape
     M, N = B * H * nc, B * H
     G = g_in.float().cumsum(dim=3)                       # [B,H,nc,C,D]
@@ -65,6 +67,8 @@ def prepare_kda_bindings(q, k, v, beta, g_in, work=torch.bfloat16) -> Dict[str, 
         "coef_ub": flat(bt.expand(B, H, nc, C, 1), C, 1),
         "coef_krest": chains(torch.exp(G_tot - G), C, D),
         "coef_S": chains(torch.exp(G_tot).reshape(B, H, nc, D, 1), D, 1),
+        "g_native": G.reshape(M, C, D).contiguous(),
+        "beta_native": beta.float().reshape(M, C).contiguous(),
     }
 
 

@@ -15,6 +15,14 @@ Keys and contracts are the reference's, so its programs and transforms name the 
   qk_prologue[_v2]                  pf_gated_qk_exec   per-channel operand prescale
   qkv_flash_native[_v2]             pf_qkv_flash_exec  chunk_o score -> output
   qkvp_flash_native[_v2]            pf_qkv_flash_exec  per-channel chunk_o flash
+  gdn_forward                       pf_gdn_exec        the whole GDN forward (two kernels)
+  kda_forward                       pf_kda_exec        the whole KDA forward (two kernels)
+
+The last two have no counterpart among the reference's keys: they are the fused forwards of
+this build (``ops.gdn_chunk_forward`` / ``ops.kda_chunk_forward``) offered to the compile stack,
+so a program the policy is allowed to collapse runs as the two fused kernels instead of its
+staged contractions.  Their workspaces are the ops module's cached ones (allocated on the first,
+eager call; a captured graph reuses them).
 
 Differences from the reference, all deliberate:
 
@@ -249,6 +257,57 @@ def _qkvp_launch(inputs, params):
 
 
 # --------------------------------------------------------------------------- #
+#  whole forwards
+# --------------------------------------------------------------------------- #
+def _per_token_gate(G: torch.Tensor) -> torch.Tensor:
+    """The within-chunk cumulative log decay G [M, C(, D)] back to the per-token gate g the fused
+    forwards take (they accumulate g inside each chunk themselves): g_0 = G_0,
+    g_i = G_i - G_(i-1)."""
+    G = G.float()
+    return torch.diff(G, dim=1, prepend=torch.zeros_like(G[:, :1]))
+
+
+def _whole_dims(q: torch.Tensor, params: dict) -> Tuple[int, int, int, int, int]:
+    B, H, nc = int(params["B"]), int(params["H"]), int(params["nc"])
+    C, D = int(params["C"]), int(params["D"])
+    if q.numel() != B * H * nc * C * D:
+        raise ValueError(f"operand of {q.numel()} elements is not [B*H*nc={B * H * nc}, C={C}, "
+                         f"D={D}]")
+    return B, H, nc, C, D
+
+
+def _gdn_forward_launch(inputs, params) -> List[torch.Tensor]:
+    """o [B,H,nc,C,D] fp32 = the GDN forward of qF, kF, vF [M,C,D] with the cumulative gate
+    g_native [M,C] and beta_native [M,C] (_gdn_full.py:103-235), through pf_gdn_exec."""
+    q, k, v, g_native, beta_native = inputs
+    B, H, nc, C, D = _whole_dims(q, params)
+    T = nc * C
+    dt = _operand_dtype(q, k, v)
+    o, _ = ops.gdn_chunk_forward(_op(q, dt, (B, H, T, D)), _op(k, dt, (B, H, T, D)),
+                                 _op(v, dt, (B, H, T, D)), _f32(beta_native, (B, H, T)),
+                                 _per_token_gate(g_native.reshape(-1, C)).reshape(B, H, T),
+                                 scale=float(params["scale"]), chunk_size=C,
+                                 output_final_state=False)
+    return [o.reshape(B, H, nc, C, D)]
+
+
+def _kda_forward_launch(inputs, params) -> List[torch.Tensor]:
+    """o [B,H,nc,C,D] fp32 = the KDA forward of qF, kF, vF [M,C,D] (bf16) with the per-channel
+    cumulative gate g_native [M,C,D] and beta_native [M,C] (_kda_full.py:42-160), through
+    pf_kda_exec."""
+    q, k, v, g_native, beta_native = inputs
+    B, H, nc, C, D = _whole_dims(q, params)
+    T = nc * C
+    bf = torch.bfloat16
+    o, _ = ops.kda_chunk_forward(_op(q, bf, (B, H, T, D)), _op(k, bf, (B, H, T, D)),
+                                 _op(v, bf, (B, H, T, D)), _f32(beta_native, (B, H, T)),
+                                 _per_token_gate(g_native.reshape(-1, C, D)).reshape(B, H, T, D),
+                                 scale=float(params["scale"]), chunk_size=C,
+                                 output_final_state=False)
+    return [o.reshape(B, H, nc, C, D)]
+
+
+# --------------------------------------------------------------------------- #
 #  the default registry
 # --------------------------------------------------------------------------- #
 def _shape_key(*names):
@@ -323,6 +382,23 @@ def default_fused_registry() -> FusedKernelRegistry:
         reg.register("qkvp_flash_native" + suffix, _Recipe(
             entry="pf_qkv_flash_exec", defines=_shape_key("nc", "H", "C", "D", "DV"),
             launch=_qkvp_launch, contract=qkvp))
+    reg.register("gdn_forward", _Recipe(
+        entry="pf_gdn_exec", defines=_shape_key("B", "H", "nc", "C", "D"),
+        launch=_gdn_forward_launch,
+        contract=FusedContract(
+            in_slots=["q", "k", "v", "g_native", "beta_native"],
+            in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
+            notes="whole GDN forward: q/k/v [M,C,D] (bf16, or fp32 end to end), cumulative "
+                  "gate g_native and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64, D = 128")))
+    reg.register("kda_forward", _Recipe(
+        entry="pf_kda_exec", defines=_shape_key("B", "H", "nc", "C", "D"),
+        launch=_kda_forward_launch,
+        contract=FusedContract(
+            in_slots=["q", "k", "v", "g_native", "beta_native"],
+            in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
+            notes="whole KDA forward: q/k/v [M,C,D] bf16, per-channel cumulative gate "
+                  "g_native [M,C,D] and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64, "
+                  "D = 128, nc >= 2")))
     return reg
 
 

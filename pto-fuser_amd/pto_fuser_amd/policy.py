@@ -4,6 +4,10 @@ Instantiates the whole transform library for the program's dims, drops what does
 asks the cost model whether each is worth trying, and orders the survivors: structural fusions
 first (they remove contractions), then the annotation levers over what remains.  It proposes;
 the compile driver decides by measurement.
+
+``Policy(whole_forward=True)`` also proposes, ahead of everything else, the whole-forward
+rewrites of this build (the canonical GDN / KDA program -> its two-kernel fused forward); the
+default pipeline is the reference's per-stage lowering.
 """
 from __future__ import annotations
 
@@ -19,6 +23,7 @@ __all__ = ["PlannedTransform", "Policy"]
 # fusions before annotation levers; the chunk_o flash before the epilogue generator (if the flash
 # is kept the generator only finds kkt, if it is dropped the generator fuses the score alone)
 _ORDER = {
+    "fuse-gdn-forward": -1, "fuse-kda-forward": -1,
     "lower-resident-scan": 0, "lower-perdim-scan": 0,
     "fuse-chunk-o-flash": 1, "fuse-perdim-chunk-o-flash": 1,
     "fuse-contraction-epilogue": 2, "batch-chunk-intra-score": 2,
@@ -37,16 +42,22 @@ class PlannedTransform:
 
 
 class Policy:
-    def __init__(self, cost: Optional[CostModel] = None) -> None:
+    def __init__(self, cost: Optional[CostModel] = None, whole_forward: bool = False) -> None:
         self.cost = cost or CostModel()
+        self.whole_forward = whole_forward
 
     def candidates(self, feat: Features) -> List[Transform]:
         from .template import FuseChunkOFlash, FuseContractionEpilogue, FusePerDimChunkOFlash
-        from .transforms import BatchChunkIntraScore, LowerPerDimScan, LowerResidentScan
+        from .transforms import (BatchChunkIntraScore, FuseGdnForward, FuseKdaForward,
+                                 LowerPerDimScan, LowerResidentScan)
         B, H, nc, C, D = feat.B, feat.H, feat.nc, feat.C, feat.D
         v2 = self.cost.predict("fuse-contraction-epilogue", feat).v2
         intra_v2 = self.cost.predict("batch-chunk-intra-score", feat).v2
-        return [
+        whole: List[Transform] = []
+        if self.whole_forward:
+            whole = [FuseGdnForward(B, H, nc, C, D, feat.dtype),
+                     FuseKdaForward(B, H, nc, C, D, feat.dtype)]
+        return whole + [
             LowerResidentScan(B, H, nc, C, D, feat.dtype),
             LowerPerDimScan(B, H, nc, C, D, feat.dtype),
             FuseChunkOFlash(B, H, nc, C, D),

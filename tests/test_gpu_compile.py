@@ -11,8 +11,8 @@ import torch
 
 from conftest import announce
 from oracle.gdn_oracle import gdn_reference, kda_reference, kkt_reference
-from pto_fuser_amd import (Features, FusedNode, GraphReplayExecutor, StagedExecutor, canonicalize,
-                           compile_program, decide, frob_rel)
+from pto_fuser_amd import (Features, FusedNode, GraphReplayExecutor, Policy, StagedExecutor,
+                           canonicalize, compile_program, decide, frob_rel)
 from pto_fuser_amd.forwards import (build_gdn_program, build_kda_program, build_kkt_fused_program,
                                     build_scan_fused_program, build_scan_staged_program,
                                     make_gdn_inputs, make_kda_inputs, make_kkt_inputs,
@@ -138,3 +138,75 @@ def test_compile_program_verified_on_device():
     torch.cuda.synchronize()
     assert _frob(o.cpu(), ref) < TOL
     print(res.report)
+
+
+def _kda(B, H, nc, C, D, seed=0):
+    inp = make_kda_inputs(B, H, nc, C, D, device=DEV, seed=seed)
+    binds = prepare_kda_bindings(inp["q"], inp["k"], inp["v"], inp["beta"], inp["g_in"])
+    T = nc * C
+    x = {n: t.double().cpu().numpy() for n, t in inp.items()}
+    ref, _ = kda_reference(x["q"].reshape(B, H, T, D), x["k"].reshape(B, H, T, D),
+                           x["v"].reshape(B, H, T, D), x["beta"].reshape(B, H, T),
+                           x["g_in"].reshape(B, H, T, D), C=C, dtype=np.float64)
+    return binds, build_kda_program(B, H, nc, C, D, D ** -0.5), ref.reshape(B, H, nc, C, D)
+
+
+@pytest.mark.parametrize("family", ["gdn", "kda"])
+def test_whole_forward_program_matches_oracle_and_staged(family):
+    """Policy(whole_forward=True) collapses the canonical program into one fused-forward node;
+    its output matches the fp64 oracle and the staged program within the bf16 bound."""
+    B, H, nc, C, D = (2, 3, 3, 64, 128) if family == "gdn" else (1, 4, 3, 64, 128)
+    announce(f"whole-forward program {family} B{B} H{H} nc{nc}")
+    binds, prog, ref = (_gdn if family == "gdn" else _kda)(B, H, nc, C, D, seed=21)
+    f = Features(B, H, nc, C, D, per_dim_gate=family == "kda")
+    whole = compile_program(prog, f, policy=Policy(whole_forward=True), verify=False).program
+    assert [n.kernel for n in whole.nodes] == [f"{family}_forward"]
+    ex = StagedExecutor()
+    o = ex.run(whole, binds)["o"]
+    staged = ex.run(canonicalize(prog), binds)["o"]
+    torch.cuda.synchronize()
+    assert o.shape == (B, H, nc, C, D) and o.dtype == torch.float32
+    assert _frob(o.cpu(), ref) < TOL, _frob(o.cpu(), ref)
+    assert frob_rel(o, staged) < TOL
+
+
+def test_whole_gdn_forward_fp32_program():
+    """fp32 work dtype: the whole-forward node runs the fused fp32 path (1e-4 relative)."""
+    B, H, nc, C, D = 1, 2, 3, 64, 128
+    announce("whole-forward program gdn fp32")
+    inp = make_gdn_inputs(B, H, nc, C, D, device=DEV, seed=22, dtype=torch.float32)
+    binds = prepare_gdn_bindings(inp["q"], inp["k"], inp["v"], inp["beta"], inp["g_in"],
+                                 work=torch.float32)
+    T = nc * C
+    x = {n: t.double().cpu().numpy() for n, t in inp.items()}
+    ref, _ = gdn_reference(x["q"].reshape(B, H, T, D), x["k"].reshape(B, H, T, D),
+                           x["v"].reshape(B, H, T, D), x["beta"].reshape(B, H, T),
+                           x["g_in"].reshape(B, H, T), C=C, dtype=np.float64)
+    prog = build_gdn_program(B, H, nc, C, D, D ** -0.5, work=torch.float32)
+    whole = compile_program(prog, Features(B, H, nc, C, D, dtype=torch.float32),
+                            policy=Policy(whole_forward=True), verify=False).program
+    o = StagedExecutor().run(whole, binds)["o"]
+    torch.cuda.synchronize()
+    got = o.double().cpu().numpy().reshape(B, H, T, D)
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-4
+
+
+@pytest.mark.parametrize("family", ["gdn", "kda"])
+def test_compile_program_keeps_whole_forward_verified(family):
+    """With bindings the driver captures the whole-forward candidate into a HIP graph, gates it
+    against the canonical program (frob, replay determinism, time) and keeps it."""
+    B, H, nc, C, D = 1, 4, 2, 64, 128
+    announce(f"compile_program verify=True whole-forward {family}")
+    binds, prog, ref = (_gdn if family == "gdn" else _kda)(B, H, nc, C, D, seed=23)
+    f = Features(B, H, nc, C, D, per_dim_gate=family == "kda")
+    res = compile_program(prog, f, policy=Policy(whole_forward=True), bindings=binds, iters=5,
+                          warmup=2)
+    first = res.report.records[0]
+    assert first.name == f"fuse-{family}-forward"
+    assert first.kept and first.frob < TOL and first.deterministic and first.faster, str(res.report)
+    assert [n.kernel for n in res.program.nodes] == [f"{family}_forward"]
+    gr = GraphReplayExecutor().capture(res.program, binds)
+    for _ in range(3):
+        out = gr.replay(binds)["o"]
+        torch.cuda.synchronize()
+        assert _frob(out.cpu(), ref) < TOL
