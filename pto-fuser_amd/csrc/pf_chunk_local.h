@@ -90,15 +90,212 @@ __device__ __forceinline__ void block_unit_lower_inverse(const float* As, float*
   }
 }
 
+// acc += M1[r1.., c1..] x M2[r2.., c2..] for 16 x 16 blocks of two fp32 LDS matrices with row
+// pitch C + 4: four 16x16x4 MFMAs in the permuted-K order (lane (c, g) supplies A row c, columns
+// 4g .. 4g+3 as one vector, and B rows 4g .. 4g+3 of column c).
+template <int CP>
+__device__ __forceinline__ floatx4 mm16(floatx4 acc, const float* M1, int r1, int c1, const float* M2,
+                                        int r2, int c2, int c, int g) {
+  const floatx4 a = *reinterpret_cast<const floatx4*>(M1 + (r1 + c) * CP + c1 + 4 * g);
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ii], M2[(r2 + 4 * g + ii) * CP + c2 + c], acc, 0, 0, 0);
+  return acc;
+}
+// acc += M1[r1.., c1..] x X with X a 16 x 16 register tile in the D layout (X[ii] = row 4g+ii,
+// column c), which is the B operand of the permuted-K chain as it stands.
+template <int CP>
+__device__ __forceinline__ floatx4 mm16r(floatx4 acc, const float* M1, int r1, int c1, const floatx4& X,
+                                         int c, int g) {
+  const floatx4 a = *reinterpret_cast<const floatx4*>(M1 + (r1 + c) * CP + c1 + 4 * g);
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ii], X[ii], acc, 0, 0, 0);
+  return acc;
+}
+template <int CP>
+__device__ __forceinline__ void put16(float* M, int r, int cc, const floatx4& X, float sign, int c, int g) {
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) M[(r + 4 * g + ii) * CP + cc + c] = sign * X[ii];
+}
+
+// (I + A)^-1 of one strictly-lower 64 x 64 block (As, fp32, pitch 68) into Ts, by 16-row blocks:
+//   1. the four diagonal blocks by forward substitution in one wave, one lane per (block,
+//      column); each row's dot product runs over four accumulators, and the strictly-lower
+//      rows are read as broadcast vectors in batches, each issued before the previous batch's
+//      rows are consumed, so the LDS latency is paid about once per batch instead of once per
+//      row;
+//   2. T10 = -T11 A10 T00 and T32 = -T33 A32 T22 (two waves);
+//   3. the lower-left 32 x 32 quadrant T_LL = -T_R (A_LL T_L), T_L / T_R the inverted upper-left
+//      / lower-right quadrants: the four 16 x 16 tiles of X = A_LL T_L (one per wave) go to the
+//      unused strictly-upper quadrant of As, then the four tiles of -T_R X.
+// The off-diagonal part is three levels of at most two dependent 16 x 16 products each (a
+// block-diagonal sweep would end in a chain of four).  Must be called by all 256 threads.
+__device__ __forceinline__ void unit_lower_inverse64(float* As, float* Ts) {
+  constexpr int CP = 64 + 4;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (w == 0) {
+    const int r = lane >> 4, cc = lane & 15;
+    const float* Ab = As + (16 * r) * CP + 16 * r;
+    // row i holds columns 0 .. i-1: ceil(i / 4) vectors; five batches of at most eight vectors
+    // (rows 1-6, 7-9, 10-11, 12-13, 14-15), two in registers at a time
+    auto row0 = [](int bt) constexpr {
+      return bt == 0 ? 1 : bt == 1 ? 7 : bt == 2 ? 10 : bt == 3 ? 12 : bt == 4 ? 14 : 16;
+    };
+    floatx4 buf[2][8];
+    auto load_batch = [&](floatx4* dst, int bt) __attribute__((always_inline)) {
+      int n = 0;
+#pragma unroll
+      for (int i = row0(bt); i < row0(bt + 1); ++i)
+#pragma unroll
+        for (int q = 0; q < (i + 3) / 4; ++q)
+          dst[n++] = *reinterpret_cast<const floatx4*>(Ab + i * CP + 4 * q);
+    };
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = (i == cc) ? 1.f : 0.f;
+    load_batch(buf[0], 0);
+#pragma unroll
+    for (int bt = 0; bt < 5; ++bt) {
+      if (bt < 4) load_batch(buf[(bt + 1) & 1], bt + 1);
+      __builtin_amdgcn_sched_barrier(0);   // keep the batch's reads ahead of this batch's math
+      const floatx4* rows = buf[bt & 1];
+      int n = 0;
+#pragma unroll
+      for (int i = row0(bt); i < row0(bt + 1); ++i) {
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < (i + 3) / 4; ++q) {
+          const floatx4 a4 = rows[n++];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (4 * q + e < i) s4[e] = fmaf(a4[e], t[4 * q + e], s4[e]);
+        }
+        const float sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        t[i] = (i > cc) ? -sum : t[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Ts[(16 * r + i) * CP + 16 * r + cc] = t[i];
+  }
+  lds_barrier();
+  if (w < 2) {   // T10 (wave 0), T32 (wave 1)
+    const int b = 32 * w;
+    const floatx4 X = mm16<CP>(zero4(), As, b + 16, b, Ts, b, b, c, g);
+    put16<CP>(Ts, b + 16, b, mm16r<CP>(zero4(), Ts, b + 16, b + 16, X, c, g), -1.f, c, g);
+  }
+  lds_barrier();
+  {  // X = A_LL T_L, tile (xa, xb) by wave 2 xa + xb, into As rows 16 xa, columns 32 + 16 xb
+    const int xa = w >> 1, xb = w & 1;
+    floatx4 X = mm16<CP>(zero4(), As, 32 + 16 * xa, 16, Ts, 16, 16 * xb, c, g);   // A_(2+xa),1 T_1,xb
+    if (xb == 0) X = mm16<CP>(X, As, 32 + 16 * xa, 0, Ts, 0, 0, c, g);           // + A_(2+xa),0 T_00
+    put16<CP>(As, 16 * xa, 32 + 16 * xb, X, 1.f, c, g);
+  }
+  lds_barrier();
+  {  // T_(2+ta),tb = -(T_(2+ta),2 X_0,tb + [ta = 1] T_33 X_1,tb)
+    const int ta = w >> 1, tb = w & 1;
+    floatx4 Y = mm16<CP>(zero4(), Ts, 32 + 16 * ta, 32, As, 0, 32 + 16 * tb, c, g);
+    if (ta == 1) Y = mm16<CP>(Y, Ts, 48, 48, As, 16, 32 + 16 * tb, c, g);
+    put16<CP>(Ts, 32 + 16 * ta, 16 * tb, Y, -1.f, c, g);
+  }
+  lds_barrier();
+}
+
+// Score blocks of the 64-token chunk (4 x 4 grid of 16-row blocks, lower triangle) owned by one
+// wave, encoded 16 qk + 4 i + j: qk = 1 for a block of P (q rows i against k rows j), 0 for a
+// block of A (k rows i against k rows j).  The lists group each wave's blocks by shared rows, so
+// a wave reads every 16-row operand block it needs once per K step and feeds it to all of its
+// MFMAs (with P: 18 operand reads per K step for the workgroup instead of 40):
+//   with P   w0: A row 3 + P(0,0)   w1: P row 3 + A(0,0)   w2: A rows 1-2   w3: P rows 1-2
+//   A only   w0: A(3,0..1)   w1: A row 2   w2: A row 1 + A(0,0)   w3: A(3,2..3)
+__device__ __forceinline__ constexpr int score_count(bool do_p, int w) {
+  return do_p ? 5 : ((w == 0 || w == 3) ? 2 : 3);
+}
+__device__ __forceinline__ constexpr int score_code(bool do_p, int w, int b) {
+  return do_p ? (w == 0   ? (b < 4 ? 12 + b : 16)
+                 : w == 1 ? (b < 4 ? 16 + 12 + b : 0)
+                 : w == 2 ? (b < 2 ? 4 + b : 8 + (b - 2))
+                          : 16 + (b < 2 ? 4 + b : 8 + (b - 2)))
+              : (w == 0   ? 12 + b
+                 : w == 1 ? 8 + b
+                 : w == 2 ? (b < 2 ? 4 + b : 0)
+                          : 14 + b);
+}
+
+// One wave's score blocks: products, then (after the workgroup barrier that frees the k / q
+// tiles) the gate / mask epilogue.  Each product is formed transposed —
+// D[4g+ii][c] = sum_d k[j][d] x[i][d] with i = 16 bi + c, j = 16 bj + 4g + ii — so a lane holds
+// four consecutive columns of one score row and stores them as one vector.
+template <typename E, int C, int DK, int KP, int CP, bool DO_P, int W>
+__device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks, const E* qs,
+                                           float* As, const float* Gs, const float* Bs, int m) {
+  constexpr int N = score_count(DO_P, W);
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  floatx4 acc[N];
+#pragma unroll
+  for (int b = 0; b < N; ++b) acc[b] = zero4();
+#pragma unroll
+  for (int kb = 0; kb < DK / Mfma<E>::KB; ++kb) {
+#pragma unroll
+    for (int b = 0; b < N; ++b) {
+      const int code = score_code(DO_P, W, b);
+      const E* jrow = ks + (16 * (code & 3) + c) * KP;
+      const E* irow = ((code & 16) ? qs : ks) + (16 * ((code >> 2) & 3) + c) * KP;
+      acc[b] = Mfma<E>::rows(acc[b], jrow, irow, kb, g);   // equal rows: one LDS read
+    }
+  }
+  lds_barrier();   // every wave is done reading k / q: A now overwrites them
+  // Gate / mask epilogue, branch free: every exponential is evaluated (clamped to <= 0, so it is
+  // finite) and the mask multiplies it in as 0 / 1 (a select would be turned back into a branch
+  // around the exponential), so no lane-divergent branch splits the wave's instruction stream.  epi_mode 0: A_ij = beta_i e^{G_i - G_j} [G_i - G_j <= 0]; 1: e^{min(G_i + log beta_i
+  // - G_j, 0)}.
+  const bool mode1 = a.epi_mode != 0;
+#pragma unroll
+  for (int b = 0; b < N; ++b) {
+    const int code = score_code(DO_P, W, b);
+    const int i = 16 * ((code >> 2) & 3) + c, j0 = 16 * (code & 3) + 4 * g;
+    const float gi = Gs[i];
+    const floatx4 gj = *reinterpret_cast<const floatx4*>(Gs + j0);
+    floatx4 out;
+    if (!(code & 16)) {
+      const float bi = Bs[i];
+      const float lb = mode1 ? __logf(bi) : 0.f, pre = mode1 ? 1.f : bi;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const float x = gi + lb - gj[ii];
+        const float e = __expf(fminf(x, 0.f));
+        const float keep = ((i > j0 + ii) && (mode1 || x <= 0.f)) ? 1.f : 0.f;
+        out[ii] = keep * pre * e * acc[b][ii];
+      }
+      *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const float e = __expf(fminf(gi - gj[ii], 0.f));
+        const float keep = (i >= j0 + ii) ? 1.f : 0.f;
+        out[ii] = keep * a.p_scale * acc[b][ii] * e;
+      }
+      store4(static_cast<E*>(a.P_out) + (size_t)m * C * C + i * C + j0, out[0], out[1], out[2], out[3]);
+    }
+  }
+}
+
+#ifndef PF_K1_PERSIST
+#define PF_K1_PERSIST 0
+#endif
+// Workgroup b takes chunks b, b + gridDim.x, ...  With kChunkLocalPersist the grid is capped at
+// what the device holds at once and the k / q tiles (and gates) of the next chunk are loaded into
+// registers at the top of each chunk, landing while its scores, epilogue and inverse run;
+// otherwise the grid has one workgroup per chunk.
+constexpr bool kChunkLocalPersist = PF_K1_PERSIST != 0;
+
 template <typename E, typename TO, int C, int DK, bool DO_P, bool DO_INV>
 __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
-  static_assert(C % 16 == 0 && C <= 64, "chunk size must be 16, 32, 48 or 64");
+  static_assert(C == 64, "the chunk-local kernel is written for 64-token chunks");
   static_assert(DK % Mfma<E>::KB == 0, "head dim must be a multiple of the MFMA K block");
   constexpr int PE = 16 / sizeof(E);
   constexpr int KP = DK + PE;   // LDS row pitch of k / q (elements)
   constexpr int CP = C + 4;     // LDS row pitch of A / T (floats)
-  constexpr int NB = C / 16;
-  constexpr int NL = NB * (NB + 1) / 2;
   constexpr int VE = Vec16<E>::N;
   constexpr int NV = C * (DK / VE);                 // 16-byte vectors per k (or q) chunk tile
   constexpr int NVT = NV / 256;                     // per thread
@@ -117,134 +314,114 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   float* As = reinterpret_cast<float*>(kqt);
   float* Ts = As + C * CP;
 
-  const int m = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
-  const size_t row0 = (size_t)m * C;
-  if (a.scale_out && m == 0 && tid == 0) *a.scale_out = a.p_scale;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
+  if (a.scale_out && blockIdx.x == 0 && tid == 0) *a.scale_out = a.p_scale;
+  const int M = a.M, stride = (int)gridDim.x;
 
-  // ---- 1. stage k (and q), gates: every load issued before the first LDS store ----------------
-  {
-    const uint4* kg = reinterpret_cast<const uint4*>(static_cast<const E*>(a.k) + row0 * DK);
-    const uint4* qg = reinterpret_cast<const uint4*>(static_cast<const E*>(a.q) + row0 * DK);
-    uint4 kr[NVT], qr[NVT];
+  u32x4 kr[NVT], qr[NVT];   // native vectors (a uint4 struct copy would go through scratch)
+  float x = 0.f, bv = 0.f;
+  // Loads of chunk m into registers; every lane loads (lanes past C repeat a row), so no branch
+  // sits around a load and the wait counts stay exact.
+  auto fetch = [&](int m) __attribute__((always_inline)) {
+    const size_t r0 = (size_t)m * C;
+    const u32x4* kg = reinterpret_cast<const u32x4*>(static_cast<const E*>(a.k) + r0 * DK);
+    const u32x4* qg = reinterpret_cast<const u32x4*>(static_cast<const E*>(a.q) + r0 * DK);
 #pragma unroll
     for (int i = 0; i < NVT; ++i) {
       kr[i] = kg[tid + 256 * i];
-      qr[i] = DO_P ? qg[tid + 256 * i] : make_uint4(0u, 0u, 0u, 0u);
+      qr[i] = DO_P ? qg[tid + 256 * i] : u32x4{0u, 0u, 0u, 0u};
     }
-    float x = 0.f, bv = 0.f;
-    if (tid < C) {
-      x = a.g != nullptr ? a.g[row0 + tid] : 0.f;
-      bv = a.beta[row0 + tid];
-    }
+    x = a.g != nullptr ? a.g[r0 + (tid & (C - 1))] : 0.f;
+    bv = a.beta[r0 + (tid & (C - 1))];
+  };
+  // k / q tiles into LDS; wave 0 forms G (within-chunk cumsum) and stages the gates.
+  auto stage = [&](int m) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NVT; ++i) {
       const int u = tid + 256 * i;
       const int r = u / (DK / VE), v = u % (DK / VE);
-      *reinterpret_cast<uint4*>(ks + r * KP + v * VE) = kr[i];
-      if (DO_P) *reinterpret_cast<uint4*>(qs + r * KP + v * VE) = qr[i];
+      *reinterpret_cast<u32x4*>(ks + r * KP + v * VE) = kr[i];
+      if (DO_P) *reinterpret_cast<u32x4*>(qs + r * KP + v * VE) = qr[i];
     }
     if (w == 0) {
+      float xs = x;
       if (!a.g_is_cumsum) {
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-          const float y = __shfl_up(x, off);
-          if (lane >= off) x += y;
+          const float y = __shfl_up(xs, off);
+          if (lane >= off) xs += y;
         }
       }
-      if (lane < C) {
-        Gs[lane] = x;
-        Bs[lane] = bv;
-        if (a.G_out) a.G_out[row0 + lane] = x;
-      }
+      Gs[lane] = xs;
+      Bs[lane] = bv;
+      if (a.G_out) a.G_out[(size_t)m * C + lane] = xs;
     }
-  }
+  };
+
+  int m = blockIdx.x;
+  fetch(m);
+  stage(m);
   lds_barrier();
-
-  // ---- 2. gated score blocks: kkt (A) and, optionally, qk (P) -------------------------------
-  // Wave w owns the blocks x = w, w+4, ... of the list [kk blocks | qk blocks]; their MFMA chains
-  // are interleaved (independent accumulators), and each product is formed transposed —
-  // D[4g+ii][c] = sum_d b[j][d] a[i][d] with i = 16 bi + c, j = 16 bj + 4g + ii — so a lane holds
-  // four consecutive columns of one score row and stores them as one vector.
-  {
-    constexpr int NSB = NL * (DO_P ? 2 : 1), NPW = (NSB + 3) / 4;
-    floatx4 acc[NPW];
-    int bI[NPW], bJ[NPW];
-    bool isqk[NPW], valid[NPW];
-#pragma unroll
-    for (int sb = 0; sb < NPW; ++sb) {
-      const int x = w + 4 * sb;
-      valid[sb] = x < NSB;
-      isqk[sb] = x >= NL;
-      int idx = isqk[sb] ? x - NL : x, bi = 0;
-      while (idx > bi) { idx -= bi + 1; ++bi; }
-      bI[sb] = valid[sb] ? bi : 0;
-      bJ[sb] = valid[sb] ? idx : 0;
-      acc[sb] = zero4();
+  for (;;) {
+    const int next = m + stride;
+    if (kChunkLocalPersist) fetch(next < M ? next : m);   // lands while this chunk runs
+    // ---- gated score blocks: kkt (A) and, optionally, qk (P) ----------------------------------
+    switch (w) {
+      case 0: score_wave<E, C, DK, KP, CP, DO_P, 0>(a, ks, qs, As, Gs, Bs, m); break;
+      case 1: score_wave<E, C, DK, KP, CP, DO_P, 1>(a, ks, qs, As, Gs, Bs, m); break;
+      case 2: score_wave<E, C, DK, KP, CP, DO_P, 2>(a, ks, qs, As, Gs, Bs, m); break;
+      default: score_wave<E, C, DK, KP, CP, DO_P, 3>(a, ks, qs, As, Gs, Bs, m); break;
     }
-#pragma unroll
-    for (int kb = 0; kb < DK / Mfma<E>::KB; ++kb) {
-#pragma unroll
-      for (int sb = 0; sb < NPW; ++sb) {
-        if (!valid[sb]) continue;
-        const E* jrow = ks + (16 * bJ[sb] + c) * KP;                    // k rows j
-        const E* irow = (isqk[sb] ? qs : ks) + (16 * bI[sb] + c) * KP;  // k or q rows i
-        acc[sb] = Mfma<E>::rows(acc[sb], jrow, irow, kb, g);
+    if (DO_P) {  // zero the strictly-upper 16x16 blocks of P (the scan reads whole K blocks)
+      uint4* P = reinterpret_cast<uint4*>(static_cast<E*>(a.P_out) + (size_t)m * C * C);
+      for (int u = tid; u < C * C / VE; u += 256) {
+        const int i = u / (C / VE), j0 = (u % (C / VE)) * VE;
+        if ((j0 >> 4) > (i >> 4)) P[u] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
-    lds_barrier();   // every wave is done reading k / q: A now overwrites them
-#pragma unroll
-    for (int sb = 0; sb < NPW; ++sb) {
-      if (!valid[sb]) continue;
-      const int i = 16 * bI[sb] + c, j0 = 16 * bJ[sb] + 4 * g;
-      const float gi = Gs[i];
-      const floatx4 gj = *reinterpret_cast<const floatx4*>(Gs + j0);
-      floatx4 out;
-      if (!isqk[sb]) {
-        const float bi = Bs[i];
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const float coef = a.epi_mode == 0 ? bi * safe_exp(gi - gj[ii])
-                                             : __expf(fminf(gi + __logf(bi) - gj[ii], 0.f));
-          out[ii] = (i > j0 + ii) ? coef * acc[sb][ii] : 0.f;
-        }
-        *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
-      } else {
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-          out[ii] = (i >= j0 + ii) ? a.p_scale * acc[sb][ii] * __expf(fminf(gi - gj[ii], 0.f)) : 0.f;
-        store4(static_cast<E*>(a.P_out) + (size_t)m * C * C + i * C + j0, out[0], out[1], out[2], out[3]);
+    lds_barrier();
+
+    if (a.A_out) {
+      float* Ao = a.A_out + (size_t)m * C * C;
+      for (int e = tid; e < C * C; e += 256) {
+        const int i = e / C, j = e % C;
+        Ao[e] = (j < i) ? As[i * CP + j] : 0.f;
       }
     }
-  }
-  if (DO_P) {  // zero the strictly-upper 16x16 blocks of P (the scan reads whole K blocks)
-    uint4* P = reinterpret_cast<uint4*>(static_cast<E*>(a.P_out) + (size_t)m * C * C);
-    for (int u = tid; u < C * C / VE; u += 256) {
-      const int i = u / (C / VE), j0 = (u % (C / VE)) * VE;
-      if ((j0 >> 4) > (i >> 4)) P[u] = make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
-  lds_barrier();
 
-  if (a.A_out) {
-    float* Ao = a.A_out + (size_t)m * C * C;
-    for (int e = tid; e < C * C; e += 256) {
-      const int i = e / C, j = e % C;
-      Ao[e] = (j < i) ? As[i * CP + j] : 0.f;
+    // ---- T (lower unit-triangular, zeros above), four columns per lane and store ------------
+    // T is read out of LDS first and stored after the next chunk is staged: the stage's wait for
+    // the prefetched loads then has no T stores ahead of it in the memory counter.
+    constexpr int NTV = DO_INV ? C * C / 4 / 256 : 0;
+    floatx4 t4[NTV > 0 ? NTV : 1];
+    if (DO_INV) {
+      unit_lower_inverse64(As, Ts);
+#pragma unroll
+      for (int it = 0; it < NTV; ++it) {
+        const int u = tid + 256 * it;
+        t4[it] = *reinterpret_cast<const floatx4*>(Ts + (u / (C / 4)) * CP + (u % (C / 4)) * 4);
+      }
     }
-  }
-
-  if (DO_INV) {
-    block_unit_lower_inverse<C>(As, Ts);
-
-    // ---- 4. write T (lower unit-triangular, zeros above), four columns per store ----------
-    TO* To = static_cast<TO*>(a.T_out) + (size_t)m * C * C;
-    for (int u = tid; u < C * C / 4; u += 256) {
-      const int i = u / (C / 4), j0 = (u % (C / 4)) * 4;
-      const floatx4 t4 = *reinterpret_cast<const floatx4*>(Ts + i * CP + j0);
-      store4(To + i * C + j0, (j0 <= i) ? t4[0] : 0.f, (j0 + 1 <= i) ? t4[1] : 0.f,
-             (j0 + 2 <= i) ? t4[2] : 0.f, (j0 + 3 <= i) ? t4[3] : 0.f);
+    auto store_t = [&](int mc) __attribute__((always_inline)) {
+      TO* To = static_cast<TO*>(a.T_out) + (size_t)mc * C * C;
+#pragma unroll
+      for (int it = 0; it < NTV; ++it) {
+        const int u = tid + 256 * it;
+        const int i = u / (C / 4), j0 = (u % (C / 4)) * 4;
+        store4(To + i * C + j0, (j0 <= i) ? t4[it][0] : 0.f, (j0 + 1 <= i) ? t4[it][1] : 0.f,
+               (j0 + 2 <= i) ? t4[it][2] : 0.f, (j0 + 3 <= i) ? t4[it][3] : 0.f);
+      }
+    };
+    if (!kChunkLocalPersist || next >= M) {
+      store_t(m);
+      break;
     }
+    lds_barrier();   // every wave has read A / T: the next chunk's k / q overwrite them
+    stage(next);
+    store_t(m);
+    m = next;
+    lds_barrier();
   }
 }
 
