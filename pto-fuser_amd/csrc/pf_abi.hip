@@ -5,7 +5,6 @@
 #include <hip/hip_runtime.h>
 
 #include <new>
-#include <type_traits>
 
 #include "../../include/pto_fuser_hip.h"
 #include "pf_chunk_local.h"
@@ -54,26 +53,6 @@ bool gdn_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
          valid_dtype(dtype);
 }
 
-// Workgroups of a persistent chunk-local launch: as many as the device holds at once (CUs times
-// the kernel's occupancy per CU), at most one per chunk.  Queried once per kernel.
-template <typename E, bool DO_P>
-unsigned chunk_local_grid(size_t M) {
-  if (!pf::kChunkLocalPersist) return (unsigned)M;
-  static int cap = 0;
-  if (cap == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(
-                &pf::chunk_local_kernel<E, std::conditional_t<DO_P, E, float>, 64, 128, DO_P, true>),
-            256, 0) != hipSuccess)
-      return (unsigned)M;   // no query: one workgroup per chunk (still correct)
-    cap = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
-  }
-  return (unsigned)(M < (size_t)cap ? M : (size_t)cap);
-}
-
 int launch_status() {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? PF_OK : static_cast<int>(e);
@@ -95,11 +74,10 @@ int chunk_local_launch(const void* q, const void* k, const float* beta, const fl
   a.P_out = base + lay.p_off;
   a.A_out = nullptr;
   a.M = static_cast<int>(M);
-  a.epi_mode = 0;
   a.g_is_cumsum = 0;
   a.p_scale = scale;
   a.scale_out = reinterpret_cast<float*>(base + lay.s_off);
-  pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3(chunk_local_grid<E, true>(M)), dim3(256), 0, stream>>>(a);
+  pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
   return launch_status();
 }
 
@@ -250,15 +228,14 @@ int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_o
   a.P_out = nullptr;
   a.A_out = A_out;
   a.M = M;
-  a.epi_mode = 0;
   a.g_is_cumsum = g_is_cumsum ? 1 : 0;
   a.p_scale = 1.f;
   a.scale_out = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PF_DTYPE_BF16)
-    pf::chunk_local_kernel<bf16, float, 64, 128, false, true><<<dim3(chunk_local_grid<bf16, false>(M)), dim3(256), 0, s>>>(a);
+    pf::chunk_local_kernel<bf16, float, 64, 128, false, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(a);
   else
-    pf::chunk_local_kernel<float, float, 64, 128, false, true><<<dim3(chunk_local_grid<float, false>(M)), dim3(256), 0, s>>>(a);
+    pf::chunk_local_kernel<float, float, 64, 128, false, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(a);
   return launch_status();
 }
 

@@ -3,20 +3,17 @@
 // For chunk m (C tokens, rows m*C .. m*C+C-1 of the flattened [B*H*T, dk] token axis):
 //   G     = cumsum_within_chunk(g)                                   (_gdn_full.py:63)
 //   A     = strictly_lower( beta_i * safe_exp(G_i - G_j) * (k_i . k_j) )  (_gdn_full.py:73-75)
-//           [epi_mode 1: exp(min(G_i + log beta_i - G_j, 0)), kkt_fused.h:154-185]
 //   T     = (I + A)^-1                                                 (_gdn_full.py:76-78)
 //   P     = p_scale * causal_incl_diag( (q_i . k_j) * exp(min(G_i - G_j, 0)) )
 //           (_gdn_full.py:91-95; the output scale of :97 is applied here, once per score element)
 //
 // Mapping on CDNA4: k and q chunk tiles are staged in LDS (row pitch padded by 16 bytes so the
-// MFMA operand reads are bank-conflict free per half wave); the 2*NB(NB+1)/2 lower-triangular
-// 16x16 score blocks are spread over the 4 waves and computed with bf16 (or fp32) MFMA; the
-// gate/mask epilogue runs in VALU on the accumulator registers.  The inverse is fp32:
-//   * the NB diagonal 16x16 blocks are inverted by forward substitution, one lane per column,
-//     all blocks at once (16*NB lanes);
-//   * off-diagonal blocks are filled level by level (block distance L = 1..NB-1) with
-//       T_ij = -T_ii * sum_{k=j}^{i-1} A_ik T_kj
-//     on fp32 MFMA (16x16x4), the product chain kept in registers via the permuted-K layout.
+// MFMA operand reads are bank-conflict free per 16 lanes); the 20 lower-triangular 16x16 score
+// blocks (10 of A, 10 of P) are split over the 4 waves in lists that share operand rows, and
+// computed with bf16 (or fp32) MFMA; the gate/mask epilogue runs branch free in VALU on the
+// accumulator registers.  The fp32 inverse (unit_lower_inverse64): the 16x16 diagonal blocks by
+// forward substitution in one wave, then the off-diagonal blocks by block doubling on fp32 MFMA
+// (16x16x4), the product chains kept in registers through the permuted-K layout.
 #pragma once
 
 #include "pf_device.h"
@@ -36,7 +33,6 @@ struct ChunkLocalArgs {
   void* P_out;          // [M, C, C]  E        (optional)
   float* A_out;         // [M, C, C]  fp32     (optional)
   int M;                // number of chunks
-  int epi_mode;         // 0: beta_i*safe_exp(G_i-G_j)   1: exp(min(G_i+log beta_i-G_j, 0))
   int g_is_cumsum;      // 1: g already holds within-chunk cumulative sums
   float p_scale;        // multiplies P (the forward's output scale)
   float* scale_out;     // if set, block 0 records p_scale here for the scan stage
@@ -247,9 +243,7 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
   lds_barrier();   // every wave is done reading k / q: A now overwrites them
   // Gate / mask epilogue, branch free: every exponential is evaluated (clamped to <= 0, so it is
   // finite) and the mask multiplies it in as 0 / 1 (a select would be turned back into a branch
-  // around the exponential), so no lane-divergent branch splits the wave's instruction stream.  epi_mode 0: A_ij = beta_i e^{G_i - G_j} [G_i - G_j <= 0]; 1: e^{min(G_i + log beta_i
-  // - G_j, 0)}.
-  const bool mode1 = a.epi_mode != 0;
+  // around the exponential), so no lane-divergent branch splits the wave's instruction stream.
 #pragma unroll
   for (int b = 0; b < N; ++b) {
     const int code = score_code(DO_P, W, b);
@@ -259,13 +253,11 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
     floatx4 out;
     if (!(code & 16)) {
       const float bi = Bs[i];
-      const float lb = mode1 ? __logf(bi) : 0.f, pre = mode1 ? 1.f : bi;
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const float x = gi + lb - gj[ii];
-        const float e = __expf(fminf(x, 0.f));
-        const float keep = ((i > j0 + ii) && (mode1 || x <= 0.f)) ? 1.f : 0.f;
-        out[ii] = keep * pre * e * acc[b][ii];
+      for (int ii = 0; ii < 4; ++ii) {   // beta_i safe_exp(G_i - G_j), strictly lower
+        const float x = gi - gj[ii];
+        const float keep = (i > j0 + ii && x <= 0.f) ? 1.f : 0.f;
+        out[ii] = keep * bi * __expf(fminf(x, 0.f)) * acc[b][ii];
       }
       *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
     } else {
@@ -280,15 +272,8 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
   }
 }
 
-#ifndef PF_K1_PERSIST
-#define PF_K1_PERSIST 0
-#endif
-// Workgroup b takes chunks b, b + gridDim.x, ...  With kChunkLocalPersist the grid is capped at
-// what the device holds at once and the k / q tiles (and gates) of the next chunk are loaded into
-// registers at the top of each chunk, landing while its scores, epilogue and inverse run;
-// otherwise the grid has one workgroup per chunk.
-constexpr bool kChunkLocalPersist = PF_K1_PERSIST != 0;
-
+// One workgroup per chunk; four workgroups fit a CU (LDS), so the HBM latency of one chunk's
+// loads overlaps the other workgroups' products and inverse.
 template <typename E, typename TO, int C, int DK, bool DO_P, bool DO_INV>
 __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   static_assert(C == 64, "the chunk-local kernel is written for 64-token chunks");
@@ -314,29 +299,24 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   float* As = reinterpret_cast<float*>(kqt);
   float* Ts = As + C * CP;
 
+  const int m = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
-  if (a.scale_out && blockIdx.x == 0 && tid == 0) *a.scale_out = a.p_scale;
-  const int M = a.M, stride = (int)gridDim.x;
+  const size_t row0 = (size_t)m * C;
+  if (a.scale_out && m == 0 && tid == 0) *a.scale_out = a.p_scale;
 
-  u32x4 kr[NVT], qr[NVT];   // native vectors (a uint4 struct copy would go through scratch)
-  float x = 0.f, bv = 0.f;
-  // Loads of chunk m into registers; every lane loads (lanes past C repeat a row), so no branch
-  // sits around a load and the wait counts stay exact.
-  auto fetch = [&](int m) __attribute__((always_inline)) {
-    const size_t r0 = (size_t)m * C;
-    const u32x4* kg = reinterpret_cast<const u32x4*>(static_cast<const E*>(a.k) + r0 * DK);
-    const u32x4* qg = reinterpret_cast<const u32x4*>(static_cast<const E*>(a.q) + r0 * DK);
+  // ---- 1. stage k (and q), gates: every load issued before the first LDS store ----------------
+  {
+    const u32x4* kg = reinterpret_cast<const u32x4*>(static_cast<const E*>(a.k) + row0 * DK);
+    const u32x4* qg = reinterpret_cast<const u32x4*>(static_cast<const E*>(a.q) + row0 * DK);
+    u32x4 kr[NVT], qr[NVT];   // native vectors (a uint4 struct copy would go through scratch)
 #pragma unroll
     for (int i = 0; i < NVT; ++i) {
       kr[i] = kg[tid + 256 * i];
       qr[i] = DO_P ? qg[tid + 256 * i] : u32x4{0u, 0u, 0u, 0u};
     }
-    x = a.g != nullptr ? a.g[r0 + (tid & (C - 1))] : 0.f;
-    bv = a.beta[r0 + (tid & (C - 1))];
-  };
-  // k / q tiles into LDS; wave 0 forms G (within-chunk cumsum) and stages the gates.
-  auto stage = [&](int m) __attribute__((always_inline)) {
+    const float x = a.g != nullptr ? a.g[row0 + (tid & (C - 1))] : 0.f;
+    const float bv = a.beta[row0 + (tid & (C - 1))];
 #pragma unroll
     for (int i = 0; i < NVT; ++i) {
       const int u = tid + 256 * i;
@@ -344,7 +324,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
       *reinterpret_cast<u32x4*>(ks + r * KP + v * VE) = kr[i];
       if (DO_P) *reinterpret_cast<u32x4*>(qs + r * KP + v * VE) = qr[i];
     }
-    if (w == 0) {
+    if (w == 0) {   // G = within-chunk cumsum of g (lane = token)
       float xs = x;
       if (!a.g_is_cumsum) {
 #pragma unroll
@@ -355,73 +335,47 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
       }
       Gs[lane] = xs;
       Bs[lane] = bv;
-      if (a.G_out) a.G_out[(size_t)m * C + lane] = xs;
+      if (a.G_out) a.G_out[row0 + lane] = xs;
     }
-  };
-
-  int m = blockIdx.x;
-  fetch(m);
-  stage(m);
+  }
   lds_barrier();
-  for (;;) {
-    const int next = m + stride;
-    if (kChunkLocalPersist) fetch(next < M ? next : m);   // lands while this chunk runs
-    // ---- gated score blocks: kkt (A) and, optionally, qk (P) ----------------------------------
-    switch (w) {
-      case 0: score_wave<E, C, DK, KP, CP, DO_P, 0>(a, ks, qs, As, Gs, Bs, m); break;
-      case 1: score_wave<E, C, DK, KP, CP, DO_P, 1>(a, ks, qs, As, Gs, Bs, m); break;
-      case 2: score_wave<E, C, DK, KP, CP, DO_P, 2>(a, ks, qs, As, Gs, Bs, m); break;
-      default: score_wave<E, C, DK, KP, CP, DO_P, 3>(a, ks, qs, As, Gs, Bs, m); break;
-    }
-    if (DO_P) {  // zero the strictly-upper 16x16 blocks of P (the scan reads whole K blocks)
-      uint4* P = reinterpret_cast<uint4*>(static_cast<E*>(a.P_out) + (size_t)m * C * C);
-      for (int u = tid; u < C * C / VE; u += 256) {
-        const int i = u / (C / VE), j0 = (u % (C / VE)) * VE;
-        if ((j0 >> 4) > (i >> 4)) P[u] = make_uint4(0u, 0u, 0u, 0u);
-      }
-    }
-    lds_barrier();
 
-    if (a.A_out) {
-      float* Ao = a.A_out + (size_t)m * C * C;
-      for (int e = tid; e < C * C; e += 256) {
-        const int i = e / C, j = e % C;
-        Ao[e] = (j < i) ? As[i * CP + j] : 0.f;
-      }
+  // ---- 2. gated score blocks: kkt (A) and, optionally, qk (P) ------------------------------------
+  switch (w) {
+    case 0: score_wave<E, C, DK, KP, CP, DO_P, 0>(a, ks, qs, As, Gs, Bs, m); break;
+    case 1: score_wave<E, C, DK, KP, CP, DO_P, 1>(a, ks, qs, As, Gs, Bs, m); break;
+    case 2: score_wave<E, C, DK, KP, CP, DO_P, 2>(a, ks, qs, As, Gs, Bs, m); break;
+    default: score_wave<E, C, DK, KP, CP, DO_P, 3>(a, ks, qs, As, Gs, Bs, m); break;
+  }
+  if (DO_P) {  // zero the strictly-upper 16x16 blocks of P (the scan reads whole K blocks)
+    uint4* P = reinterpret_cast<uint4*>(static_cast<E*>(a.P_out) + (size_t)m * C * C);
+    for (int u = tid; u < C * C / VE; u += 256) {
+      const int i = u / (C / VE), j0 = (u % (C / VE)) * VE;
+      if ((j0 >> 4) > (i >> 4)) P[u] = make_uint4(0u, 0u, 0u, 0u);
     }
+  }
+  lds_barrier();
 
-    // ---- T (lower unit-triangular, zeros above), four columns per lane and store ------------
-    // T is read out of LDS first and stored after the next chunk is staged: the stage's wait for
-    // the prefetched loads then has no T stores ahead of it in the memory counter.
-    constexpr int NTV = DO_INV ? C * C / 4 / 256 : 0;
-    floatx4 t4[NTV > 0 ? NTV : 1];
-    if (DO_INV) {
-      unit_lower_inverse64(As, Ts);
-#pragma unroll
-      for (int it = 0; it < NTV; ++it) {
-        const int u = tid + 256 * it;
-        t4[it] = *reinterpret_cast<const floatx4*>(Ts + (u / (C / 4)) * CP + (u % (C / 4)) * 4);
-      }
+  if (a.A_out) {
+    float* Ao = a.A_out + (size_t)m * C * C;
+    for (int e = tid; e < C * C; e += 256) {
+      const int i = e / C, j = e % C;
+      Ao[e] = (j < i) ? As[i * CP + j] : 0.f;
     }
-    auto store_t = [&](int mc) __attribute__((always_inline)) {
-      TO* To = static_cast<TO*>(a.T_out) + (size_t)mc * C * C;
+  }
+
+  if (DO_INV) {
+    unit_lower_inverse64(As, Ts);
+    // ---- 3. write T (lower unit-triangular, zeros above), four columns per store ---------------
+    TO* To = static_cast<TO*>(a.T_out) + (size_t)m * C * C;
 #pragma unroll
-      for (int it = 0; it < NTV; ++it) {
-        const int u = tid + 256 * it;
-        const int i = u / (C / 4), j0 = (u % (C / 4)) * 4;
-        store4(To + i * C + j0, (j0 <= i) ? t4[it][0] : 0.f, (j0 + 1 <= i) ? t4[it][1] : 0.f,
-               (j0 + 2 <= i) ? t4[it][2] : 0.f, (j0 + 3 <= i) ? t4[it][3] : 0.f);
-      }
-    };
-    if (!kChunkLocalPersist || next >= M) {
-      store_t(m);
-      break;
+    for (int it = 0; it < C * C / 4 / 256; ++it) {
+      const int u = tid + 256 * it;
+      const int i = u / (C / 4), j0 = (u % (C / 4)) * 4;
+      const floatx4 t4 = *reinterpret_cast<const floatx4*>(Ts + i * CP + j0);
+      store4(To + i * C + j0, (j0 <= i) ? t4[0] : 0.f, (j0 + 1 <= i) ? t4[1] : 0.f,
+             (j0 + 2 <= i) ? t4[2] : 0.f, (j0 + 3 <= i) ? t4[3] : 0.f);
     }
-    lds_barrier();   // every wave has read A / T: the next chunk's k / q overwrite them
-    stage(next);
-    store_t(m);
-    m = next;
-    lds_barrier();
   }
 }
 

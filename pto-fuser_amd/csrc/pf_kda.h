@@ -52,6 +52,47 @@ __device__ __forceinline__ int kda_swz(int r, int col) {
   return r * KP + 4 * ((col >> 2) ^ ((r >> 2) & 3)) + (col & 3);
 }
 
+// One wave's score blocks of the KDA chunk (the GDN kernel's lists, score_code): products over
+// the swizzled a / b / qe tiles, then the mask epilogue (A scaled by beta_i into LDS, P to global).
+template <int C, int KP, int CP, int W>
+__device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, const bf16* qt, float* As,
+                                               const float* Bs, bf16* P) {
+  constexpr int N = score_count(true, W);
+  const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int rd = c * KP + 4 * (g ^ ((c >> 2) & 3));   // row c, K groups g and g+4 of each 32-block
+  floatx4 acc[N];
+#pragma unroll
+  for (int b = 0; b < N; ++b) acc[b] = zero4();
+#pragma unroll
+  for (int kb = 0; kb < 128 / 32; ++kb) {
+#pragma unroll
+    for (int b = 0; b < N; ++b) {
+      const int code = score_code(true, W, b);
+      const bf16* jp = bt + 16 * (code & 3) * KP + rd + 32 * kb;
+      const bf16* ip = ((code & 16) ? qt : at) + 16 * ((code >> 2) & 3) * KP + rd + 32 * kb;
+      const bf16x8 ja = cat8(*reinterpret_cast<const bf16x4*>(jp), *reinterpret_cast<const bf16x4*>(jp + 16));
+      const bf16x8 ib = cat8(*reinterpret_cast<const bf16x4*>(ip), *reinterpret_cast<const bf16x4*>(ip + 16));
+      acc[b] = mfma_bf16(ja, ib, acc[b]);   // equal rows: one LDS read
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < N; ++b) {
+    const int code = score_code(true, W, b);
+    const int i = 16 * ((code >> 2) & 3) + c, j0 = 16 * (code & 3) + 4 * g;
+    floatx4 out;
+    if (!(code & 16)) {
+      const float bi = Bs[i];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) out[ii] = (i > j0 + ii) ? bi * acc[b][ii] : 0.f;
+      *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) out[ii] = (i >= j0 + ii) ? acc[b][ii] : 0.f;
+      store4(P + i * C + j0, out[0], out[1], out[2], out[3]);
+    }
+  }
+}
+
 template <int C, int DK, int DV>
 __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   static_assert(C == 64 && DK == 128 && DV == 128, "the KDA kernels are written for C 64, dk = dv = 128");
@@ -165,55 +206,17 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   lds_barrier();
 
   // ---- 4. scores: A = beta_i (a b^T) strictly lower (fp32, LDS), P = causal_incl(qe b^T) --------
-  // Wave w owns the blocks x = w, w+4, ... of [A blocks | P blocks]; each product is formed
-  // transposed (D[4g+ii][c] = b_j . x_i with i = 16 bI + c, j = 16 bJ + 4g + ii) so a lane holds
-  // four consecutive columns of one score row.  Both operands are read in the same (swizzled,
-  // permuted) K order.
+  // The 20 lower 16x16 blocks are split over the waves as in the GDN chunk-local kernel (lists
+  // that share operand rows: b rows on the j side of every block, a rows for A and qe rows for
+  // P on the i side), each product formed transposed so a lane holds four consecutive columns
+  // of one score row.
+  switch (__builtin_amdgcn_readfirstlane(w)) {
+    case 0: kda_score_wave<C, KP, CP, 0>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
+    case 1: kda_score_wave<C, KP, CP, 1>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
+    case 2: kda_score_wave<C, KP, CP, 2>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
+    default: kda_score_wave<C, KP, CP, 3>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
+  }
   {
-    constexpr int NB = C / 16, NL = NB * (NB + 1) / 2, NSB = 2 * NL, NPW = (NSB + 3) / 4;
-    floatx4 acc[NPW];
-    int bI[NPW], bJ[NPW];
-    bool isp[NPW], valid[NPW];
-#pragma unroll
-    for (int sb = 0; sb < NPW; ++sb) {
-      const int x = w + 4 * sb;
-      valid[sb] = x < NSB;
-      isp[sb] = x >= NL;
-      int idx = isp[sb] ? x - NL : x, bi = 0;
-      while (idx > bi) { idx -= bi + 1; ++bi; }
-      bI[sb] = valid[sb] ? bi : 0;
-      bJ[sb] = valid[sb] ? idx : 0;
-      acc[sb] = zero4();
-    }
-    const int rd = c * KP + 4 * (g ^ ((c >> 2) & 3));   // row c, K groups g and g+4 of each 32-block
-#pragma unroll
-    for (int kb = 0; kb < DK / 32; ++kb) {
-#pragma unroll
-      for (int sb = 0; sb < NPW; ++sb) {
-        if (!valid[sb]) continue;
-        const bf16* jp = bt + 16 * bJ[sb] * KP + rd + 32 * kb;
-        const bf16* ip = (isp[sb] ? qt : at) + 16 * bI[sb] * KP + rd + 32 * kb;
-        const bf16x8 ja = cat8(*reinterpret_cast<const bf16x4*>(jp), *reinterpret_cast<const bf16x4*>(jp + 16));
-        const bf16x8 ib = cat8(*reinterpret_cast<const bf16x4*>(ip), *reinterpret_cast<const bf16x4*>(ip + 16));
-        acc[sb] = mfma_bf16(ja, ib, acc[sb]);
-      }
-    }
-#pragma unroll
-    for (int sb = 0; sb < NPW; ++sb) {
-      if (!valid[sb]) continue;
-      const int i = 16 * bI[sb] + c, j0 = 16 * bJ[sb] + 4 * g;
-      floatx4 out;
-      if (!isp[sb]) {
-        const float bi = Bs[i];
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) out[ii] = (i > j0 + ii) ? bi * acc[sb][ii] : 0.f;
-        *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
-      } else {
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) out[ii] = (i >= j0 + ii) ? acc[sb][ii] : 0.f;
-        store4(a.P + (size_t)m * C * C + i * C + j0, out[0], out[1], out[2], out[3]);
-      }
-    }
     // zero the strictly-upper 16x16 blocks of P (stage 2 reads whole K blocks)
     uint4* Pz = reinterpret_cast<uint4*>(a.P + (size_t)m * C * C);
     for (int u = tid; u < C * C / 8; u += 256) {
@@ -224,7 +227,7 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   lds_barrier();
 
   // ---- 5. T = (I + A)^-1 (fp32) ------------------------------------------------------------
-  block_unit_lower_inverse<C>(As, Ts);
+  unit_lower_inverse64(As, Ts);
 
   // ---- 6. T diag(beta) as bf16 (in A's space), the v tile (in b's space) -------------------
   for (int u = tid; u < C * C / 4; u += 256) {
