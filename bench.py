@@ -17,8 +17,11 @@ Besides the required fields the line carries:
     HBM / MFMA fractions;
   * ``cpu_baseline`` — the CPU oracle (a restatement of the reference's per-(b,h,c) loop, fp32
     numpy, one BLAS thread) timed on this host over the same seeded inputs;
-  * ``secondary`` — the fused KDA forward (per-channel decay) at its benchmark configuration
-    B=2, H=32, T=8192, timed the same way (not the headline; skipped with --no-secondary).
+  * ``secondary`` — the other benchmark configurations, each timed the same way (events around
+    each call on the launch stream; not the headline; skipped with --no-secondary): the fused
+    KDA forward (per-channel decay) at B=2, H=32, T=8192; the GDN long-context forward B=1,
+    H=32, T=32768 with an initial state; the fp32 kkt + inverse over 4096 chunks; the fp32
+    DeltaNet forward B=1, H=4, T=512.
 """
 from __future__ import annotations
 
@@ -123,6 +126,71 @@ def kda_model(B, H, T, C, DK, DV):
             "compulsory_bytes": compulsory}
 
 
+def _event_ms(run, steps: int, warmup: int) -> float:
+    """Mean HIP-event time of ``run`` over ``steps`` calls on the current stream, after warmup."""
+    import torch
+    for _ in range(warmup):
+        run()
+    stream = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for e in evs:
+        e[0].record(stream)
+        run()
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    return statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+
+
+def gdn_config_secondary(B, H, T, dtype_name, h0_std, steps, warmup, kind="gdn"):
+    """The fused forward at another configuration (GDN long context with h0; fp32 DeltaNet)."""
+    import torch
+    from pto_fuser_amd.forwards import make_delta_inputs
+    from pto_fuser_amd.ops import gdn_chunk_forward, gdn_workspace
+    dev = torch.device("cuda:0")
+    C, DK, DV = 64, 128, 128
+    dtype = torch.bfloat16 if dtype_name == "bf16" else torch.float32
+    d = make_delta_inputs(B, H, T, DK, DV, kind=kind, dtype=dtype, seed=4, h0_std=h0_std,
+                          device=dev)
+    o = torch.empty(B, H, T, DV, device=dev, dtype=torch.float32)
+    hf = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32)
+    ws = gdn_workspace(B, H, T, C, DK, DV, dtype, dev)
+    ms = _event_ms(lambda: gdn_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"],
+                                             out=o, final_out=hf, workspace=ws), steps, warmup)
+    m = stage_model(B, H, T, C, DK, DV, 2 if dtype_name == "bf16" else 4)
+    nbytes = m["chunk_local"]["bytes"] + m["scan_output"]["bytes"] + (
+        B * H * DK * DV * 4 if h0_std is not None else 0)
+    if kind == "deltanet":      # no gate to read in stage 1 (stage 2 still reads the zero G)
+        nbytes -= B * H * T * 4
+    flops = m["chunk_local"]["flops"] + m["scan_output"]["flops"]
+    return {"workload": f"{'DeltaNet' if kind == 'deltanet' else 'GDN'} chunked forward B{B} H{H} "
+                        f"T{T} C64 dk128 dv128, {dtype_name} in"
+                        f"{', h0' if h0_std is not None else ''}, fp32 state/accum/o",
+            "B": B, "H": H, "T": T, "dtype": dtype_name, "ms_per_step": round(ms, 5),
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "chains": B * H,
+            "chunks_per_chain": T // C, "bytes": nbytes,
+            "hbm_frac": round(nbytes / (ms * 1e-3) / PEAK_HBM, 4),
+            "mfma_frac": round(flops / (ms * 1e-3) / (PEAK_BF16 if dtype_name == "bf16" else PEAK_FP32), 4)}
+
+
+def kkt_inverse_secondary(steps, warmup):
+    """fp32 gated kkt + (I + A)^-1 over 4096 independent 64-token chunks (returns T only)."""
+    import torch
+    from pto_fuser_amd.forwards import make_delta_inputs
+    from pto_fuser_amd.ops import kkt_inverse
+    dev = torch.device("cuda:0")
+    M, C, D = 4096, 64, 128
+    d = make_delta_inputs(1, 1, M * C, D, D, kind="gdn", dtype=torch.float32, seed=3, device=dev)
+    k, g, beta = d["k"].reshape(M * C, D), d["g"].reshape(-1), d["beta"].reshape(-1)
+    ms = _event_ms(lambda: kkt_inverse(k, g, beta), steps, warmup)
+    nbytes = M * (C * D * 4 + 2 * C * 4 + C * C * 4)      # k, g, beta in; T out
+    flops = M * (2 * C * C * D + C ** 3 / 3)
+    return {"workload": "gated kkt + unit-lower inverse, fp32, 4096 chunks C64 dk128 (T out)",
+            "M": M, "ms_per_step": round(ms, 5), "chunks_per_s": round(M / (ms * 1e-3), 1),
+            "bytes": nbytes, "hbm_frac": round(nbytes / (ms * 1e-3) / PEAK_HBM, 4),
+            "mfma_fp32_frac": round(flops / (ms * 1e-3) / PEAK_FP32, 4)}
+
+
 def kda_secondary(steps: int, warmup: int):
     """Fused KDA forward at KDA_WORKLOAD: events around each forward on the launch stream."""
     import torch
@@ -165,7 +233,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
-    ap.add_argument("--no-secondary", action="store_true", help="skip the KDA secondary record")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the secondary records")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run three plain device copies of MIB MiB: the "
                          "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -286,7 +354,15 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         line["calibration_copy_bytes"] = n * 4
     if not args.no_secondary:
-        line["secondary"] = {"kda_config5": kda_secondary(args.steps, args.warmup)}
+        sec_steps = max(1, min(args.steps, 20))
+        line["secondary"] = {
+            "kda_config5": kda_secondary(args.steps, args.warmup),
+            "gdn_config4_long_context": gdn_config_secondary(1, 32, 32768, "bf16", 0.02, sec_steps,
+                                                             min(args.warmup, 5)),
+            "kkt_inverse_config3": kkt_inverse_secondary(sec_steps, min(args.warmup, 5)),
+            "deltanet_config1": gdn_config_secondary(1, 4, 512, "fp32", None, sec_steps,
+                                                     min(args.warmup, 5), kind="deltanet"),
+        }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(inputs, runs=args.cpu_runs)
     print(json.dumps(line), flush=True)
