@@ -81,6 +81,20 @@ int chunk_local_launch(const void* q, const void* k, const float* beta, const fl
   return launch_status();
 }
 
+// CUs of the current device (queried once; 256 on MI355X if the query fails).
+int device_cu_count() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
 template <typename E>
 int scan_output_launch(const void* q, const void* k, const void* v, const float* beta,
                        const float* h0, float* o, float* h_final, int BH, int NC,
@@ -106,10 +120,16 @@ int scan_output_launch(const void* q, const void* k, const void* v, const float*
   const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
   if constexpr (std::is_same<E, bf16>::value) {
     // bf16: row-major staging read back through LDS transpose loads (gfx950); its loader
-    // pipeline assumes at least two chunks per chain, a single chunk takes the generic kernel
+    // pipeline assumes at least two chunks per chain, a single chunk takes the generic kernel.
+    // One workgroup per (chain, 32-column slice) and CU; when that leaves CUs idle (fewer than
+    // 8 chains per 32 CUs: long sequences at small batch) the slices are 16 columns wide, one
+    // compute wave each, so twice the workgroups run the same chains.
     constexpr int NLW = PF_TR_LOADER_WAVES, NWT = PF_TR_COMPUTE_WAVES, NCB = 2 / NWT;
     static_assert(NWT * NCB == 2, "the bf16 scan kernel covers 32 state columns per workgroup");
-    if (NC >= 2)
+    if (NC >= 2 && (size_t)BH * (DV / 32) < (size_t)device_cu_count())
+      pf::scan_output_tr_kernel<C, DK, DV, 1, NLW, 1>
+          <<<dim3((unsigned)(BH * (DV / 16))), dim3(64 * (1 + NLW)), 0, stream>>>(a);
+    else if (NC >= 2)
       pf::scan_output_tr_kernel<C, DK, DV, NWT, NLW, NCB><<<dim3(grid), dim3(64 * (NWT + NLW)), 0, stream>>>(a);
     else
       pf::scan_output_kernel<E, C, DK, DV, NWC, 1>

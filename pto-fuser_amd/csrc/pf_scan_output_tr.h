@@ -98,7 +98,7 @@ __device__ __forceinline__ floatx4 mfma_bf16(const bf16x8& a, const bf16x8& b, c
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// LDS image of one chunk, C = 64, DK = 128, tile width TW = 32.
+// LDS image of one chunk, C = 64, DK = 128, tile width TW = 32 or 16.
 template <int C, int DK, int TW>
 struct TrStage {
   static constexpr int KP = DK + 16;   // k, q: Swz<2,3>
@@ -117,10 +117,12 @@ struct TrStage {
 };
 
 // Loader register image of one chunk; NLW loader waves share the tile (k, q: 1024 vectors;
-// T, P: 512; v: 256 — per thread NK, NTP, NV).
-template <int NLW>
+// T, P: 512; v: 8 TW — per thread NK, NTP, NV; with fewer v vectors than loader lanes the extra
+// lanes repeat a vector's load and skip its store).
+template <int NLW, int TW>
 struct TrRegs {
-  static constexpr int NK = 1024 / (64 * NLW), NTP = 512 / (64 * NLW), NV = 256 / (64 * NLW);
+  static constexpr int NK = 1024 / (64 * NLW), NTP = 512 / (64 * NLW);
+  static constexpr int NV = (8 * TW + 64 * NLW - 1) / (64 * NLW);
   uint4 k[NK], q[NK], t[NTP], p[NTP], v[NV];
   float vb[NV];   // beta of each v row this lane stages
   float g, b;
@@ -138,11 +140,11 @@ __global__ __launch_bounds__(64 * (NWC + NLW)) __attribute__((amdgpu_waves_per_e
 void scan_output_tr_kernel(ScanOutArgs a) {
   constexpr int TW = 16 * NWC * NCB;
   using Stage = TrStage<C, DK, TW>;
-  using Regs = TrRegs<NLW>;
+  using Regs = TrRegs<NLW, TW>;
   constexpr int KP = Stage::KP, TP = Stage::TP, BP = Stage::BP;
   constexpr int NT = DV / TW;
-  static_assert(C == 64 && DK == 128 && TW == 32 && (NLW == 2 || NLW == 4),
-                "tile shapes of the transpose-read kernel are fixed: C 64, DK 128, 32-column tile");
+  static_assert(C == 64 && DK == 128 && (TW == 32 || TW == 16) && (NLW == 2 || NLW == 4),
+                "tile shapes of the transpose-read kernel: C 64, DK 128, 32- or 16-column tile");
 
   __shared__ __attribute__((aligned(16))) Stage st[2];
   // o of chunk c (fp32, [C][OP]) is staged in ost[c & 1] by the compute waves and written to HBM
@@ -206,8 +208,12 @@ void scan_output_tr_kernel(ScanOutArgs a) {
     const uint32_t tp_voff = (uint32_t)(trow_l * C + tvec * 8) * 2;
     const int tp_lds = trow_l * TP + 8 * tvec;
     auto trow_i = [](int i) -> int { return NLW == 2 ? ((i & 1) << 3) | (((i >> 1) & 1) << 5) : ((i & 1) << 3); };
-    // v (4 vectors per row of the tile): row = (lt >> 2) + (16*NLW) i, columns 8 vvec .. +7
-    const int vrow_l = lt >> 2, vvec = lt & 3;
+    // v (TW / 8 vectors per row of the tile): vector u = lt + 64 NLW i, row = u / (TW / 8),
+    // columns 8 vvec .. +7; lanes past the tile's 8 TW vectors repeat one (load only)
+    constexpr int VPR = TW / 8, V_VECS = C * VPR, VSTEP = 64 * NLW / VPR;
+    const int vu = lt % V_VECS;
+    const bool v_owner = V_VECS >= 64 * NLW || lt < V_VECS;
+    const int vrow_l = vu / VPR, vvec = vu % VPR;
     const uint32_t v_voff = (uint32_t)(vrow_l * DV + col0 + vvec * 8) * 2;
     float Lrun = 0.f;                                   // log of the state factor f_c
 
@@ -229,8 +235,8 @@ void scan_output_tr_kernel(ScanOutArgs a) {
       const uint32_t v_s = (uint32_t)ch * C * DV * 2;
 #pragma unroll
       for (int i = 0; i < Regs::NV; ++i) {
-        r.v[i] = buf_load16(rv, v_voff, v_s + (uint32_t)(16 * NLW * i) * DV * 2);
-        r.vb[i] = Bc[(size_t)ch * C + vrow_l + 16 * NLW * i];
+        r.v[i] = buf_load16(rv, v_voff, v_s + (uint32_t)(VSTEP * i) * DV * 2);
+        r.vb[i] = Bc[(size_t)ch * C + vrow_l + VSTEP * i];
       }
       // every lane loads (lanes past the first loader wave repeat its rows): no branch around a
       // load, so the compiler's wait counts stay exact and two chunks stay in flight
@@ -250,13 +256,15 @@ void scan_output_tr_kernel(ScanOutArgs a) {
         put16(s.ts + tp_lds + rowi * TP, r.t[i], (i & 1) != 0);
         put16(s.ps + tp_lds + rowi * TP, r.p[i], (i & 1) != 0);
       }
+      if (v_owner) {
 #pragma unroll
-      for (int i = 0; i < Regs::NV; ++i) {
-        const int row = vrow_l + 16 * NLW * i;
-        const bf16x8 x = __builtin_bit_cast(bf16x8, r.v[i]);
-        const int prow = (((row >> 2) ^ (2 * vvec)) << 2) | (row & 3);
+        for (int i = 0; i < Regs::NV; ++i) {
+          const int row = vrow_l + VSTEP * i;
+          const bf16x8 x = __builtin_bit_cast(bf16x8, r.v[i]);
+          const int prow = (((row >> 2) ^ (2 * vvec)) << 2) | (row & 3);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s.bv[(vvec * 8 + e) * BP + prow] = (float)x[e] * r.vb[i];
+          for (int e = 0; e < 8; ++e) s.bv[(vvec * 8 + e) * BP + prow] = (float)x[e] * r.vb[i];
+        }
       }
       // gate tables with the deferred state factor f_c = e^{Lrun}
       const float gl = __shfl(r.g, C - 1);                // G_last (log of the chunk decay)
@@ -276,15 +284,16 @@ void scan_output_tr_kernel(ScanOutArgs a) {
       Lrun = Lnext;
     };
 
-    // o rows of a staged chunk: 8 16-byte vectors per row, two per loader thread
-    const int orow_l = lt >> 3, oseg = lt & 7;
+    // o rows of a staged chunk: TW / 4 16-byte vectors per row, C TW / (256 NLW) per thread
+    constexpr int OPR = TW / 4;
+    const int orow_l = lt / OPR, oseg = lt % OPR;
     const uint32_t o_voff = (uint32_t)(orow_l * DV + col0 + 4 * oseg) * 4;
     auto store_o = [&](const float* os, int ch) {
 #pragma unroll
       for (int i = 0; i < (C * TW / 4) / (64 * NLW); ++i) {
-        const int row = orow_l + (64 * NLW / 8) * i;
+        const int row = orow_l + (64 * NLW / OPR) * i;
         const floatx4 x = *reinterpret_cast<const floatx4*>(os + row * OP + 4 * oseg);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro, o_voff + (uint32_t)((64 * NLW / 8) * i * DV) * 4,
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro, o_voff + (uint32_t)((64 * NLW / OPR) * i * DV) * 4,
                                                (uint32_t)ch * C * DV * 4, 0);
       }
     };
