@@ -50,7 +50,7 @@ METRIC = "GDN chunked-forward tokens/sec at B=4,H=16,T=4096 bf16; % MFMA/HBM roo
 COUNTER_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
 MEASURED_KIB = {
     "scan_output": {"FETCH_SIZE": 132212.0, "WRITE_SIZE": 135168.0},
-    "chunk_local": {"FETCH_SIZE": 66656.9, "WRITE_SIZE": 66568.1},
+    "chunk_local": {"FETCH_SIZE": 66655.9, "WRITE_SIZE": 58368.8},
 }
 
 
@@ -65,14 +65,16 @@ def stage_model(B, H, T, C, DK, DV, esize):
     """Algorithmic flops and HBM bytes per launch of the two kernels.
 
     Unit = one (b,h) chunk of C tokens; a launch processes M = B*H*T/C units.
-      stage 1 (chunk-local): reads k, q (2*C*DK*e) + g, beta (2*C*4); writes T, P (2*C*C*e) +
+      stage 1 (chunk-local): reads k, q (2*C*DK*e) + g, beta (2*C*4); writes T (C*C*e), P
+               (the 10 lower 16x16 blocks and the 2 upper ones the scan reads: 12*256*e) and
                G (C*4).  flops: k k^T and q k^T (2 * 2*C*C*DK) + inverse (C^3/3).
       stage 2 (scan+output): reads q, k, v (2*C*DK*e + C*DV*e), T, P (2*C*C*e), G, beta
                (2*C*4); writes o (C*DV*4); plus the final state (DK*DV*4) once per chain.
                flops: k S, q S, k^T v_new (3 * 2*C*DK*DV) + T r, P v_new (2 * 2*C*C*DV).
     """
     M = B * H * (T // C)
-    s1_bytes = 2 * C * DK * esize + 2 * C * 4 + 2 * C * C * esize + C * 4
+    p_blocks = (C // 16) * (C // 16 + 1) // 2 + 2           # lower blocks + (0,1), (2,3)
+    s1_bytes = 2 * C * DK * esize + 2 * C * 4 + C * C * esize + p_blocks * 256 * esize + C * 4
     s1_flops = 2 * (2 * C * C * DK) + C ** 3 / 3
     s2_bytes = (2 * C * DK + C * DV) * esize + 2 * C * C * esize + 2 * C * 4 + C * DV * 4
     s2_flops = 3 * (2 * C * DK * DV) + 2 * (2 * C * C * DV)
@@ -115,10 +117,12 @@ KDA_WORKLOAD = dict(B=2, H=32, T=8192, C=64, DK=128, DV=128)
 def kda_model(B, H, T, C, DK, DV):
     """Algorithmic HBM bytes of the fused KDA forward per chunk of C tokens (bf16 operands):
     stage 1 reads q, k, v (bf16), g (fp32 per channel), beta and writes W, U, QE, KR (bf16),
-    P (bf16), the chunk decay (fp32); stage 2 reads W, QE, KR, U, P, the decay and writes o
+    P (bf16: the lower 16x16 blocks and the two upper ones stage 2 reads), the chunk decay
+    (fp32); stage 2 reads W, QE, KR, U, P (whole), the decay and writes o
     (fp32).  ``compulsory`` is what any forward must move: q, k, v, g, beta in, o out."""
     M = B * H * (T // C)
-    s1 = 3 * C * DK * 2 + C * DK * 4 + C * 4 + 4 * C * DK * 2 + C * C * 2 + DK * 4
+    p_blocks = (C // 16) * (C // 16 + 1) // 2 + 2           # lower blocks + (0,1), (2,3)
+    s1 = 3 * C * DK * 2 + C * DK * 4 + C * 4 + 4 * C * DK * 2 + p_blocks * 256 * 2 + DK * 4
     s2 = 4 * C * DK * 2 + C * C * 2 + DK * 4 + C * DV * 4
     final = B * H * DK * DV * 4
     compulsory = M * (3 * C * DK * 2 + C * DK * 4 + C * 4 + C * DV * 4) + final

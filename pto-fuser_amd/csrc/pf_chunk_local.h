@@ -270,6 +270,12 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
       store4(static_cast<E*>(a.P_out) + (size_t)m * C * C + i * C + j0, out[0], out[1], out[2], out[3]);
     }
   }
+  if (DO_P && (W == 0 || W == 3)) {
+    // the strictly-upper blocks of P that the scan kernels read as parts of a 32-wide K block:
+    // (0,1) beside P(0,0) (wave 0) and (2,3) beside P row 2 (wave 3); the other four are never read
+    const int i = (W == 0 ? 0 : 32) + c, j0 = (W == 0 ? 16 : 48) + 4 * g;
+    store4(static_cast<E*>(a.P_out) + (size_t)m * C * C + i * C + j0, 0.f, 0.f, 0.f, 0.f);
+  }
 }
 
 // One workgroup per chunk; four workgroups fit a CU (LDS), so the HBM latency of one chunk's
@@ -346,13 +352,6 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
     case 1: score_wave<E, C, DK, KP, CP, DO_P, 1>(a, ks, qs, As, Gs, Bs, m); break;
     case 2: score_wave<E, C, DK, KP, CP, DO_P, 2>(a, ks, qs, As, Gs, Bs, m); break;
     default: score_wave<E, C, DK, KP, CP, DO_P, 3>(a, ks, qs, As, Gs, Bs, m); break;
-  }
-  if (DO_P) {  // zero the strictly-upper 16x16 blocks of P (the scan reads whole K blocks)
-    uint4* P = reinterpret_cast<uint4*>(static_cast<E*>(a.P_out) + (size_t)m * C * C);
-    for (int u = tid; u < C * C / VE; u += 256) {
-      const int i = u / (C / VE), j0 = (u % (C / VE)) * VE;
-      if ((j0 >> 4) > (i >> 4)) P[u] = make_uint4(0u, 0u, 0u, 0u);
-    }
   }
   lds_barrier();
 

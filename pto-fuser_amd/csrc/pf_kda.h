@@ -40,7 +40,7 @@ struct KdaLocalArgs {
   bf16* U;              // [M, C, DV]  T diag(beta) v
   bf16* QE;             // [M*C, DK]   scale q e^G
   bf16* KR;             // [M*C, DK]   k e^{G_last - G}
-  bf16* P;              // [M, C, C]   causal_incl(QE (k e^-G)^T), zero strictly-upper 16x16 blocks
+  bf16* P;              // [M, C, C]   causal_incl(QE (k e^-G)^T); upper blocks (0,1), (2,3) zero
   float* DEC;           // [M, DK]     e^{G_last}
 };
 
@@ -90,6 +90,10 @@ __device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, c
       for (int ii = 0; ii < 4; ++ii) out[ii] = (i >= j0 + ii) ? acc[b][ii] : 0.f;
       store4(P + i * C + j0, out[0], out[1], out[2], out[3]);
     }
+  }
+  if (W == 0 || W == 3) {   // the upper blocks (0,1) and (2,3) the scan reads; see score_wave
+    const int i = (W == 0 ? 0 : 32) + c, j0 = (W == 0 ? 16 : 48) + 4 * g;
+    store4(P + i * C + j0, 0.f, 0.f, 0.f, 0.f);
   }
 }
 
@@ -215,14 +219,6 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
     case 1: kda_score_wave<C, KP, CP, 1>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
     case 2: kda_score_wave<C, KP, CP, 2>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
     default: kda_score_wave<C, KP, CP, 3>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
-  }
-  {
-    // zero the strictly-upper 16x16 blocks of P (stage 2 reads whole K blocks)
-    uint4* Pz = reinterpret_cast<uint4*>(a.P + (size_t)m * C * C);
-    for (int u = tid; u < C * C / 8; u += 256) {
-      const int i = u / (C / 8), j0 = (u % (C / 8)) * 8;
-      if ((j0 >> 4) > (i >> 4)) Pz[u] = make_uint4(0u, 0u, 0u, 0u);
-    }
   }
   lds_barrier();
 
