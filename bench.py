@@ -49,8 +49,8 @@ METRIC = "GDN chunked-forward tokens/sec at B=4,H=16,T=4096 bf16; % MFMA/HBM roo
 # figures are recorded here and must be re-measured whenever a kernel's memory access changes.
 COUNTER_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
 MEASURED_KIB = {
-    "scan_output": {"FETCH_SIZE": 132212.0, "WRITE_SIZE": 135168.0},
-    "chunk_local": {"FETCH_SIZE": 66655.9, "WRITE_SIZE": 58368.8},
+    "scan_output": {"FETCH_SIZE": 132214.4, "WRITE_SIZE": 135168.0},
+    "chunk_local": {"FETCH_SIZE": 66657.0, "WRITE_SIZE": 50176.9},
 }
 
 
@@ -65,16 +65,19 @@ def stage_model(B, H, T, C, DK, DV, esize):
     """Algorithmic flops and HBM bytes per launch of the two kernels.
 
     Unit = one (b,h) chunk of C tokens; a launch processes M = B*H*T/C units.
-      stage 1 (chunk-local): reads k, q (2*C*DK*e) + g, beta (2*C*4); writes T (C*C*e), P
-               (the 10 lower 16x16 blocks and the 2 upper ones the scan reads: 12*256*e) and
-               G (C*4).  flops: k k^T and q k^T (2 * 2*C*C*DK) + inverse (C^3/3).
-      stage 2 (scan+output): reads q, k, v (2*C*DK*e + C*DV*e), T, P (2*C*C*e), G, beta
-               (2*C*4); writes o (C*DV*4); plus the final state (DK*DV*4) once per chain.
+      stage 1 (chunk-local): reads k, q (2*C*DK*e) + g, beta (2*C*4); writes T and P without
+               the upper-right quadrant no kernel reads ((C*C - (C/2)^2)*e each; P's two other
+               upper 16x16 blocks are not written either: 12*256*e) and G (C*4).  flops: k k^T
+               and q k^T (2 * 2*C*C*DK) + inverse (C^3/3).
+      stage 2 (scan+output): reads q, k, v (2*C*DK*e + C*DV*e), T, P (2*C*C*e: the unread
+               quadrant shares its 128-byte lines with the rows' read halves), G, beta (2*C*4);
+               writes o (C*DV*4); plus the final state (DK*DV*4) once per chain.
                flops: k S, q S, k^T v_new (3 * 2*C*DK*DV) + T r, P v_new (2 * 2*C*C*DV).
     """
     M = B * H * (T // C)
     p_blocks = (C // 16) * (C // 16 + 1) // 2 + 2           # lower blocks + (0,1), (2,3)
-    s1_bytes = 2 * C * DK * esize + 2 * C * 4 + C * C * esize + p_blocks * 256 * esize + C * 4
+    tp_tile = C * C - (C // 2) ** 2                         # T / P elements any kernel reads
+    s1_bytes = 2 * C * DK * esize + 2 * C * 4 + tp_tile * esize + p_blocks * 256 * esize + C * 4
     s1_flops = 2 * (2 * C * C * DK) + C ** 3 / 3
     s2_bytes = (2 * C * DK + C * DV) * esize + 2 * C * C * esize + 2 * C * 4 + C * DV * 4
     s2_flops = 3 * (2 * C * DK * DV) + 2 * (2 * C * C * DV)

@@ -75,6 +75,7 @@ int chunk_local_launch(const void* q, const void* k, const float* beta, const fl
   a.A_out = nullptr;
   a.M = static_cast<int>(M);
   a.g_is_cumsum = 0;
+  a.t_lower_only = 1;   // the scan kernels read T's rows 0..31 up to column 31 only
   a.p_scale = scale;
   a.scale_out = reinterpret_cast<float*>(base + lay.s_off);
   pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
@@ -249,6 +250,7 @@ int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_o
   a.A_out = A_out;
   a.M = M;
   a.g_is_cumsum = g_is_cumsum ? 1 : 0;
+  a.t_lower_only = 0;   // T_out is the caller's: the whole matrix, zeros above the diagonal
   a.p_scale = 1.f;
   a.scale_out = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);

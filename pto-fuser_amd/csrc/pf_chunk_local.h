@@ -34,6 +34,8 @@ struct ChunkLocalArgs {
   float* A_out;         // [M, C, C]  fp32     (optional)
   int M;                // number of chunks
   int g_is_cumsum;      // 1: g already holds within-chunk cumulative sums
+  int t_lower_only;     // 1: leave T's upper-right quadrant (rows < 32, columns >= 32, all zero)
+                        //    unwritten: the fused forward's scan never reads it
   float p_scale;        // multiplies P (the forward's output scale)
   float* scale_out;     // if set, block 0 records p_scale here for the scan stage
 };
@@ -371,6 +373,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
     for (int it = 0; it < C * C / 4 / 256; ++it) {
       const int u = tid + 256 * it;
       const int i = u / (C / 4), j0 = (u % (C / 4)) * 4;
+      if (a.t_lower_only && i < 32 && j0 >= 32) continue;
       const floatx4 t4 = *reinterpret_cast<const floatx4*>(Ts + i * CP + j0);
       store4(To + i * C + j0, (j0 <= i) ? t4[0] : 0.f, (j0 + 1 <= i) ? t4[1] : 0.f,
              (j0 + 2 <= i) ? t4[2] : 0.f, (j0 + 3 <= i) ? t4[3] : 0.f);

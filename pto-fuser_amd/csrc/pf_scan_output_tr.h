@@ -208,6 +208,9 @@ void scan_output_tr_kernel(ScanOutArgs a) {
     const uint32_t tp_voff = (uint32_t)(trow_l * C + tvec * 8) * 2;
     const int tp_lds = trow_l * TP + 8 * tvec;
     auto trow_i = [](int i) -> int { return NLW == 2 ? ((i & 1) << 3) | (((i >> 1) & 1) << 5) : ((i & 1) << 3); };
+    // (T's upper-right quadrant, rows < 32 and columns >= 32, is staged with the rest of each
+    // 128-byte row but never used: the products of rows 0..31 stop at K block 0, and K1 leaves it
+    // unwritten.)
     // v (TW / 8 vectors per row of the tile): vector u = lt + 64 NLW i, row = u / (TW / 8),
     // columns 8 vvec .. +7; lanes past the tile's 8 TW vectors repeat one (load only)
     constexpr int VPR = TW / 8, V_VECS = C * VPR, VSTEP = 64 * NLW / VPR;

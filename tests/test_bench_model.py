@@ -14,10 +14,13 @@ def test_stage_model_per_chunk_bytes_and_flops():
     m = bench.stage_model(4, 16, 4096, C, DK, DV, 2)
     s1, s2 = m["chunk_local"], m["scan_output"]
     assert s1["units"] == s2["units"] == 4 * 16 * 64
-    # stage 1: k, q (bf16) + g, beta in; T (bf16), 12 P blocks (bf16), G out
-    assert s1["bytes_per_unit"] == 2 * C * DK * 2 + 2 * C * 4 + C * C * 2 + 12 * 16 * 16 * 2 + C * 4
-    # stage 2: q, k, v, T, P (bf16) + G, beta in; o (fp32) out; plus the final state per chain
-    assert s2["bytes_per_unit"] == 98816
+    # stage 1: k, q (bf16) + g, beta in; T without its upper-right quadrant and 12 P blocks
+    # (bf16), G out
+    tp = C * C - 32 * 32
+    assert s1["bytes_per_unit"] == 2 * C * DK * 2 + 2 * C * 4 + tp * 2 + 12 * 16 * 16 * 2 + C * 4
+    # stage 2: q, k, v, T, P (bf16, whole 128-byte rows) + G, beta in; o (fp32) out; plus the
+    # final state per chain
+    assert s2["bytes_per_unit"] == (2 * C * DK + C * DV) * 2 + 2 * C * C * 2 + 2 * C * 4 + C * DV * 4 == 98816
     assert s2["bytes"] == 4096 * 98816 + 64 * DK * DV * 4
     # flops per chunk: kk^T + qk^T + inverse; kS, qS, k^T v_new + T r, P v_new
     assert s1["flops_per_unit"] == pytest.approx(4 * C * C * DK + C ** 3 / 3)
