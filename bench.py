@@ -12,13 +12,17 @@ launches only.  ``value`` is tokens/s = B*T*K / t over exactly K steps bracketed
 Besides the required fields the line carries:
   * ``roofline`` — the dominant kernel's achieved algorithmic HBM bandwidth against the MI355X
     peak, from HIP events recorded around each launch on the launch stream inside the timed
-    region (per-unit bytes: see ``stage_model``);
+    region (per-unit bytes: see ``stage_model``).  Events are recorded on a sample of about ten
+    evenly spaced steps, not on every step: three event records per step add ≈ 10 µs to a
+    ≈ 140 µs forward (measured), which would understate ``value``; the sampled kernels run in
+    the same stream order as the rest;
   * ``stages`` — both kernels' average durations, algorithmic bytes and flops, and their
     HBM / MFMA fractions;
   * ``cpu_baseline`` — the CPU oracle (a restatement of the reference's per-(b,h,c) loop, fp32
     numpy, one BLAS thread) timed on this host over the same seeded inputs;
-  * ``secondary`` — the other benchmark configurations, each timed the same way (events around
-    each call on the launch stream; not the headline; skipped with --no-secondary): the fused
+  * ``secondary`` — the other benchmark configurations, each timed over back-to-back calls
+    bracketed by one event pair on the launch stream (not the headline; skipped with
+    --no-secondary): the fused
     KDA forward (per-channel decay) at B=2, H=32, T=8192; the GDN long-context forward B=1,
     H=32, T=32768 with an initial state; the fp32 kkt + inverse over 4096 chunks; the fp32
     DeltaNet forward B=1, H=4, T=512.
@@ -134,19 +138,21 @@ def kda_model(B, H, T, C, DK, DV):
 
 
 def _event_ms(run, steps: int, warmup: int) -> float:
-    """Mean HIP-event time of ``run`` over ``steps`` calls on the current stream, after warmup."""
+    """Time per call of ``run`` over ``steps`` back-to-back calls on the current stream, after
+    warmup: one HIP event pair brackets the whole loop (an event record between calls would add
+    its own few microseconds to every call)."""
     import torch
     for _ in range(warmup):
         run()
     stream = torch.cuda.current_stream()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    for e in evs:
-        e[0].record(stream)
+    e0.record(stream)
+    for _ in range(steps):
         run()
-        e[1].record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
-    return statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    return e0.elapsed_time(e1) / steps
 
 
 def gdn_config_secondary(B, H, T, dtype_name, h0_std, steps, warmup, kind="gdn"):
@@ -199,7 +205,7 @@ def kkt_inverse_secondary(steps, warmup):
 
 
 def kda_secondary(steps: int, warmup: int):
-    """Fused KDA forward at KDA_WORKLOAD: events around each forward on the launch stream."""
+    """Fused KDA forward at KDA_WORKLOAD, timed like the other secondary records."""
     import torch
     from pto_fuser_amd.forwards import make_delta_inputs
     from pto_fuser_amd.ops import kda_chunk_forward, kda_workspace
@@ -211,17 +217,7 @@ def kda_secondary(steps: int, warmup: int):
     ws = kda_workspace(B, H, T, C, DK, DV, torch.bfloat16, dev)
     run = lambda: kda_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], out=o,  # noqa: E731
                                     final_out=hf, workspace=ws)
-    for _ in range(warmup):
-        run()
-    stream = torch.cuda.current_stream(dev)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
-    torch.cuda.synchronize()
-    for e in evs:
-        e[0].record(stream)
-        run()
-        e[1].record(stream)
-    torch.cuda.synchronize()
-    ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    ms = _event_ms(run, steps, warmup)
     m = kda_model(B, H, T, C, DK, DV)
     return {"workload": "KDA chunked forward B2 H32 T8192 C64 dk128 dv128, per-channel decay, "
                         "bf16 in, fp32 state/accum/o", **KDA_WORKLOAD,
@@ -236,8 +232,9 @@ def kda_secondary(steps: int, warmup: int):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50,
+                    help="untimed forwards first (the clock takes a few ms of load to settle)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
     ap.add_argument("--no-secondary", action="store_true", help="skip the secondary records")
@@ -296,16 +293,19 @@ def main(argv=None) -> int:
 
     for _ in range(args.warmup):
         step()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # per-kernel events on every `stride`-th timed step (about ten samples)
+    stride = max(1, args.steps // 10)
+    events = {i: [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+              for i in range(0, args.steps, stride)}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(events[i])
+        step(events.get(i))
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) / args.steps * 1e3
-    k1_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
-    k2_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in events)
+    k1_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events.values())
+    k2_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in events.values())
 
     model = stage_model(B, H, T, C, DK, DV, esize=2)
     stages = {}
@@ -338,6 +338,7 @@ def main(argv=None) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "event_samples": len(events),
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -361,14 +362,14 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         line["calibration_copy_bytes"] = n * 4
     if not args.no_secondary:
-        sec_steps = max(1, min(args.steps, 20))
+        sec_steps, sec_warm = max(1, min(args.steps, 50)), min(args.warmup, 10)
         line["secondary"] = {
-            "kda_config5": kda_secondary(args.steps, args.warmup),
+            "kda_config5": kda_secondary(sec_steps, sec_warm),
             "gdn_config4_long_context": gdn_config_secondary(1, 32, 32768, "bf16", 0.02, sec_steps,
-                                                             min(args.warmup, 5)),
-            "kkt_inverse_config3": kkt_inverse_secondary(sec_steps, min(args.warmup, 5)),
+                                                             sec_warm),
+            "kkt_inverse_config3": kkt_inverse_secondary(sec_steps, sec_warm),
             "deltanet_config1": gdn_config_secondary(1, 4, 512, "fp32", None, sec_steps,
-                                                     min(args.warmup, 5), kind="deltanet"),
+                                                     sec_warm, kind="deltanet"),
         }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(inputs, runs=args.cpu_runs)
