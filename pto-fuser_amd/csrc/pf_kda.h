@@ -389,13 +389,13 @@ void kda_scan_kernel(KdaScanArgs a) {
 #pragma unroll
       for (int i = 0; i < Regs::NK; ++i) {
         const uint32_t rowi = krow_i(i);
-        r.w[i] = buf_load16_sw(rw, k_voff, k_s + rowi * DK * 2, (i & 1) != 0);
-        r.q[i] = buf_load16_sw(rq, k_voff, k_s + rowi * DK * 2, (i & 1) != 0);
-        r.k[i] = buf_load16_sw(rk, k_voff, k_s + rowi * DK * 2, (i & 1) != 0);
+        r.w[i] = buf_load16(rw, k_voff, k_s + rowi * DK * 2);
+        r.q[i] = buf_load16(rq, k_voff, k_s + rowi * DK * 2);
+        r.k[i] = buf_load16(rk, k_voff, k_s + rowi * DK * 2);
       }
       const uint32_t p_s = (uint32_t)ch * C * C * 2;
 #pragma unroll
-      for (int i = 0; i < Regs::NP; ++i) r.p[i] = buf_load16_sw(rp, p_voff, p_s + prow_i(i) * C * 2, (i & 1) != 0);
+      for (int i = 0; i < Regs::NP; ++i) r.p[i] = buf_load16(rp, p_voff, p_s + prow_i(i) * C * 2);
       const uint32_t u_s = (uint32_t)ch * C * DV * 2;
 #pragma unroll
       for (int i = 0; i < Regs::NU; ++i) r.u[i] = buf_load16(ru, u_voff, u_s + (uint32_t)(16 * NLW * i) * DV * 2);

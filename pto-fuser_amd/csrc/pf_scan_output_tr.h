@@ -51,19 +51,11 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// A 16-byte row vector bound for a Swz<RS,1> tile slot whose 8-byte halves are swapped when
-// `swap` (a compile-time constant at every call): the halves are loaded straight into the swapped
-// register positions, so the LDS store is a plain, conflict-free 16-byte write with no register
-// shuffle (a shuffle would wait for the load to land, and split 8-byte stores conflict).
-#ifndef PF_TR_SWAP_MODE
-#define PF_TR_SWAP_MODE 2
-#endif
-__device__ __forceinline__ uint4 buf_load16_sw(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
-                                               bool swap) {
-  if (!swap || PF_TR_SWAP_MODE != 0) return buf_load16(r, voff, soff);
-  const auto lo = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
-  const auto hi = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 8, soff, 0);
-  return make_uint4(hi[0], hi[1], lo[0], lo[1]);
+// Store of a 16-byte row vector into a Swz<RS,1> tile slot whose 8-byte halves are swapped when
+// `swap` (a compile-time constant at every call): the halves change places in registers and the
+// LDS store stays one conflict-free 16-byte write (two 8-byte stores would conflict).
+__device__ __forceinline__ void put16(bf16* dst, const uint4& x, bool swap) {
+  *reinterpret_cast<uint4*>(dst) = swap ? make_uint4(x.z, x.w, x.x, x.y) : x;
 }
 
 // Transposed 8-byte LDS read (see the header comment); p is an LDS address.
@@ -71,18 +63,6 @@ __device__ __forceinline__ bf16x4 lds_read_tr(const bf16* p) {
   const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) i16x4*)(const_cast<bf16*>(p)));
   return __builtin_bit_cast(bf16x4, v);
-}
-
-__device__ __forceinline__ void put16(bf16* dst, const uint4& x, bool swap) {
-  if (!swap || PF_TR_SWAP_MODE == 0) {
-    *reinterpret_cast<uint4*>(dst) = x;
-  } else if (PF_TR_SWAP_MODE == 1) {
-    *reinterpret_cast<uint2*>(dst + 4) = make_uint2(x.x, x.y);
-    __asm__ __volatile__("" ::: "memory");
-    *reinterpret_cast<uint2*>(dst) = make_uint2(x.z, x.w);
-  } else {
-    *reinterpret_cast<uint4*>(dst) = make_uint4(x.z, x.w, x.x, x.y);
-  }
 }
 
 __device__ __forceinline__ bf16x8 cat8(const bf16x4& lo, const bf16x4& hi) {
@@ -225,15 +205,15 @@ void scan_output_tr_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int i = 0; i < Regs::NK; ++i) {
         const uint32_t rowi = krow_i(i);
-        r.k[i] = buf_load16_sw(rk, kq_voff, kq_s + rowi * DK * 2, (i & 1) != 0);   // Swz<2,3>: i0
-        r.q[i] = buf_load16_sw(rq, kq_voff, kq_s + rowi * DK * 2, (i & 1) != 0);
+        r.k[i] = buf_load16(rk, kq_voff, kq_s + rowi * DK * 2);
+        r.q[i] = buf_load16(rq, kq_voff, kq_s + rowi * DK * 2);
       }
       const uint32_t tp_s = (uint32_t)ch * C * C * 2;
 #pragma unroll
       for (int i = 0; i < Regs::NTP; ++i) {
         const uint32_t rowi = trow_i(i);
-        r.t[i] = buf_load16_sw(rt, tp_voff, tp_s + rowi * C * 2, (i & 1) != 0);    // Swz<3,1>: i0
-        r.p[i] = buf_load16_sw(rp, tp_voff, tp_s + rowi * C * 2, (i & 1) != 0);
+        r.t[i] = buf_load16(rt, tp_voff, tp_s + rowi * C * 2);
+        r.p[i] = buf_load16(rp, tp_voff, tp_s + rowi * C * 2);
       }
       const uint32_t v_s = (uint32_t)ch * C * DV * 2;
 #pragma unroll
