@@ -14,6 +14,12 @@
 #ifndef PF_TR_LOADER_WAVES
 #define PF_TR_LOADER_WAVES 4
 #endif
+// loader waves of the 16-column variant (one compute wave): two are faster there (long-context
+// GDN, B1 H32 T32768: 0.861 vs 0.896 ms), four for the 32-column kernel (headline: 0.159 vs
+// 0.168 ms)
+#ifndef PF_TR16_LOADER_WAVES
+#define PF_TR16_LOADER_WAVES 2
+#endif
 // compute waves of the bf16 scan kernel; each owns 2 / PF_TR_COMPUTE_WAVES blocks of 16 columns
 #ifndef PF_TR_COMPUTE_WAVES
 #define PF_TR_COMPUTE_WAVES 2
@@ -125,11 +131,12 @@ int scan_output_launch(const void* q, const void* k, const void* v, const float*
     // One workgroup per (chain, 32-column slice) and CU; when that leaves CUs idle (fewer than
     // 8 chains per 32 CUs: long sequences at small batch) the slices are 16 columns wide, one
     // compute wave each, so twice the workgroups run the same chains.
-    constexpr int NLW = PF_TR_LOADER_WAVES, NWT = PF_TR_COMPUTE_WAVES, NCB = 2 / NWT;
+    constexpr int NLW = PF_TR_LOADER_WAVES, NLW16 = PF_TR16_LOADER_WAVES;
+    constexpr int NWT = PF_TR_COMPUTE_WAVES, NCB = 2 / NWT;
     static_assert(NWT * NCB == 2, "the bf16 scan kernel covers 32 state columns per workgroup");
     if (NC >= 2 && (size_t)BH * (DV / 32) < (size_t)device_cu_count())
-      pf::scan_output_tr_kernel<C, DK, DV, 1, NLW, 1>
-          <<<dim3((unsigned)(BH * (DV / 16))), dim3(64 * (1 + NLW)), 0, stream>>>(a);
+      pf::scan_output_tr_kernel<C, DK, DV, 1, NLW16, 1>
+          <<<dim3((unsigned)(BH * (DV / 16))), dim3(64 * (1 + NLW16)), 0, stream>>>(a);
     else if (NC >= 2)
       pf::scan_output_tr_kernel<C, DK, DV, NWT, NLW, NCB><<<dim3(grid), dim3(64 * (NWT + NLW)), 0, stream>>>(a);
     else
