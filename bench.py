@@ -16,6 +16,9 @@ Besides the required fields the line carries:
     evenly spaced steps, not on every step: three event records per step add ≈ 10 µs to a
     ≈ 140 µs forward (measured), which would understate ``value``; the sampled kernels run in
     the same stream order as the rest;
+    ``roofline.device_copy_GBps`` is a plain 256 MiB device copy timed after the headline in the
+    same process (read + write bytes per second), and ``frac_of_device_copy`` the dominant
+    kernel's rate against it: what the datasheet fraction leaves to the memory system itself;
   * ``stages`` — both kernels' average durations, algorithmic bytes and flops, and their
     HBM / MFMA fractions;
   * ``cpu_baseline`` — the CPU oracle (a restatement of the reference's per-(b,h,c) loop, fp32
@@ -153,6 +156,17 @@ def _event_ms(run, steps: int, warmup: int) -> float:
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def device_copy_GBps(mib: int = 256, reps: int = 20) -> float:
+    """HBM rate of a plain device-to-device copy of `mib` MiB (bytes read + written per second),
+    timed like the secondary records: a practical ceiling to read the kernels' figures against."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda:0", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    ms = _event_ms(lambda: dst.copy_(src), reps, 3)
+    return 2 * n * 4 / (ms * 1e-3) / 1e9
 
 
 def gdn_config_secondary(B, H, T, dtype_name, h0_std, steps, warmup, kind="gdn"):
@@ -328,6 +342,9 @@ def main(argv=None) -> int:
                 "traffic": measured_traffic(dom), "algorithmic_bytes": ds["bytes"]}
     for name in stages:
         stages[name]["traffic"] = measured_traffic(name)
+    copy_GBps = device_copy_GBps()
+    roofline["device_copy_GBps"] = round(copy_GBps, 1)
+    roofline["frac_of_device_copy"] = round(ds["hbm_GBps"] / copy_GBps, 4)
     total_bytes = sum(model[n]["bytes"] for n in model)
     total_flops = sum(model[n]["flops"] for n in model)
 
