@@ -85,3 +85,16 @@ def test_kda_deterministic():
     o1, h1 = _run(inp)
     o2, h2 = _run(inp)
     assert np.array_equal(o1, o2) and np.array_equal(h1, h2)
+
+
+def test_kda_linear_in_v_config5():
+    """Size-independent property at config 5's full size: o and the final state are linear in v,
+    bit for bit.  Doubling v is exact in bf16, and both KDA kernels only scale by it (U = T(beta
+    v) stored in bf16, the fp32 MFMA accumulations, the bf16 packing of the state), each step
+    commuting with a factor of two."""
+    announce("KDA bf16 linearity in v B2 H32 T8192")
+    inp = make_delta_inputs(2, 32, 8192, kind="kda", dtype=torch.bfloat16, seed=5)
+    o1, h1 = _run(inp)
+    o2, h2 = _run(dict(inp, v=inp["v"] * 2))
+    assert np.array_equal(o2, 2 * o1), max_abs(o2, 2 * o1)
+    assert np.array_equal(h2, 2 * h1), max_abs(h2, 2 * h1)
