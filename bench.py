@@ -7,28 +7,33 @@ fp32 accumulation/state/output) through the C-ABI library: stage 1 (chunk-local 
 (I+A)^-1, gated qk^T) and stage 2 (state scan fused with the output).  Inputs are resident in
 HBM before timing starts; outputs and the workspace are preallocated, so the timed region is
 launches only.  ``value`` is tokens/s = B*T*K / t over exactly K steps bracketed by
-``torch.cuda.synchronize()``.
+``torch.cuda.synchronize()``, with nothing else recorded inside the loop.
+
+Order of one run: the CPU baseline (a child process, before this process touches the GPU); a
+256 MiB device-copy rate (a practical HBM ceiling measured in the same run); W warmup steps; the K
+timed steps; then a separate pass of ``--event-steps`` forwards with HIP events around each
+kernel on the launch stream, which gives the per-kernel durations; then the secondary
+configurations.
 
 Besides the required fields the line carries:
-  * ``roofline`` — the dominant kernel's achieved algorithmic HBM bandwidth against the MI355X
-    peak, from HIP events recorded around each launch on the launch stream inside the timed
-    region (per-unit bytes: see ``stage_model``).  Events are recorded on a sample of about ten
-    evenly spaced steps, not on every step: three event records per step add ≈ 10 µs to a
-    ≈ 140 µs forward (measured), which would understate ``value``; the sampled kernels run in
-    the same stream order as the rest;
-    ``roofline.device_copy_GBps`` is a plain 256 MiB device copy timed after the headline in the
-    same process (read + write bytes per second), and ``frac_of_device_copy`` the dominant
-    kernel's rate against it: what the datasheet fraction leaves to the memory system itself;
-  * ``stages`` — both kernels' average durations, algorithmic bytes and flops, and their
-    HBM / MFMA fractions;
-  * ``cpu_baseline`` — the CPU oracle (a restatement of the reference's per-(b,h,c) loop, fp32
-    numpy, one BLAS thread) timed on this host over the same seeded inputs;
+  * ``roofline`` — the dominant kernel (stage 2) against the MI355X HBM peak.  ``achieved`` is
+    the forward's compulsory bytes (q, k, v, beta, g in, o and the final state out: 83 456 B per
+    64-token chunk x 4096 chunks = 341.8 MB) over the kernel's event-timed average duration:
+    stage 2 reads every input the forward needs and writes o and the state.  ``own_*`` are the
+    same figures on the bytes stage 2 itself moves (it also reads T, P and G from stage 1's
+    workspace: 98 816 B per chunk + the final state).  ``traffic`` is the counter-measured HBM
+    bytes per launch recorded in profiles/hbm_traffic_gdn_forward.json, reported only when that
+    record was taken from the library built from the current sources (its source hash), else
+    null;
+  * ``stages`` — both kernels' average durations, bytes and flops, and their HBM / MFMA fractions;
+  * ``forward`` — the whole forward's compulsory-byte and flop fractions at ``ms_per_step``;
+  * ``cpu_baseline`` — the fp32 numpy oracle (the reference's per-(b,h,c) loop) on this host's
+    cores (oracle/cpu_baseline.py), with a one-core figure beside it;
   * ``secondary`` — the other benchmark configurations, each timed over back-to-back calls
-    bracketed by one event pair on the launch stream (not the headline; skipped with
-    --no-secondary): the fused
-    KDA forward (per-channel decay) at B=2, H=32, T=8192; the GDN long-context forward B=1,
-    H=32, T=32768 with an initial state; the fp32 kkt + inverse over 4096 chunks; the fp32
-    DeltaNet forward B=1, H=4, T=512.
+    bracketed by one event pair on the launch stream (skipped with --no-secondary): the fused
+    KDA forward at B=2, H=32, T=8192; the GDN long-context forward B=1, H=32, T=32768 with an
+    initial state; the fp32 kkt + inverse over 4096 chunks; the fp32 DeltaNet forward B=1, H=4,
+    T=512.
 """
 from __future__ import annotations
 
@@ -36,6 +41,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -48,24 +54,33 @@ PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
 PEAK_BF16 = 2.5e15         # dense bf16 MFMA, flop/s
 PEAK_FP32 = 157.3e12       # dense fp32 MFMA, flop/s
 METRIC = "GDN chunked-forward tokens/sec at B=4,H=16,T=4096 bf16; % MFMA/HBM roofline"
-
-# HBM bytes per launch at WORKLOAD, measured with two rocprofv3 counter passes over this script
-# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch; profiles/hbm_traffic_gdn_forward.md gives the
-# commands) and scaled by what the same counters read for a plain 256 MiB device copy
-# (FETCH_SIZE x2.0, WRITE_SIZE x1.0).  A counter run cannot happen inside the timed bench, so the
-# figures are recorded here and must be re-measured whenever a kernel's memory access changes.
-COUNTER_SCALE = {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0}
-MEASURED_KIB = {
-    "scan_output": {"FETCH_SIZE": 132214.4, "WRITE_SIZE": 135168.0},
-    "chunk_local": {"FETCH_SIZE": 66657.0, "WRITE_SIZE": 50176.9},
-}
+COUNTERS = os.path.join(ROOT, "profiles", "hbm_traffic_gdn_forward.json")
 
 
-def measured_traffic(kernel):
-    kib = MEASURED_KIB.get(kernel)
+def measured_traffic(kernel, lib_hash):
+    """HBM bytes per launch of ``kernel`` from the recorded counter passes (FETCH_SIZE and
+    WRITE_SIZE in KiB per dispatch, each scaled by what it reads for a plain copy of known
+    size), or None when no record exists for the library built from the current sources."""
+    try:
+        with open(COUNTERS) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("source_hash") != lib_hash:
+        return None
+    kib = rec.get("kernels", {}).get(kernel)
     if kib is None:
         return None
-    return int(sum(kib[c] * COUNTER_SCALE[c] * 1024 for c in kib))
+    return int(sum(kib[c] * rec["scale"][c] * 1024 for c in ("FETCH_SIZE", "WRITE_SIZE")))
+
+
+def compulsory_bytes(B, H, T, DK, DV, esize, h0=False, g_channels=1):
+    """What any forward must move: q, k, v (esize bytes each) + beta and g (fp32; g has
+    g_channels values per token) in, o (fp32) and the final state (fp32) out, h0 if given."""
+    n = B * H * T
+    state = B * H * DK * DV * 4
+    return (n * (2 * DK + DV) * esize + n * 4 * (1 + g_channels) + n * DV * 4 + state
+            + (state if h0 else 0))
 
 
 def stage_model(B, H, T, C, DK, DV, esize):
@@ -96,29 +111,16 @@ def stage_model(B, H, T, C, DK, DV, esize):
     }
 
 
-def cpu_baseline(inputs, runs: int = 3):
-    """Time the CPU oracle (reference loop structure, fp32) on the full workload, one BLAS
-    thread; median of ``runs`` after a one-chain warmup."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
-    from oracle.gdn_oracle import gdn_reference
-
-    x = {n: (None if t is None else t.float().numpy()) for n, t in inputs.items()}
-    B, H, T = x["beta"].shape
-    times = []
-    with threadpool_limits(1):
-        gdn_reference(x["q"][:1, :1], x["k"][:1, :1], x["v"][:1, :1], x["beta"][:1, :1],
-                      x["g"][:1, :1], C=WORKLOAD["C"], dtype=np.float32, loop=True)
-        for _ in range(runs):
-            t0 = time.perf_counter()
-            gdn_reference(x["q"], x["k"], x["v"], x["beta"], x["g"], C=WORKLOAD["C"],
-                          dtype=np.float32, loop=True)
-            times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"value": B * T / t, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": (f"full workload B{B} H{H} T{T} (all {B * H} chains x {T // WORKLOAD['C']} "
-                       f"chunks), numpy fp32 oracle in the reference's b,h,c loop order, "
-                       f"1 BLAS thread, median of {runs} runs ({', '.join(f'{s:.2f}' for s in times)} s)")}
+def cpu_baseline(runs: int = 5, timeout: float = 600.0):
+    """The CPU oracle timed on this host's cores (oracle/cpu_baseline.py, run as a child process
+    so that its worker pool forks from a process that has not initialised the GPU)."""
+    cmd = [sys.executable, "-m", "oracle.cpu_baseline", "--B", str(WORKLOAD["B"]),
+           "--H", str(WORKLOAD["H"]), "--T", str(WORKLOAD["T"]), "--C", str(WORKLOAD["C"]),
+           "--runs", str(runs)]
+    r = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"cpu baseline failed ({r.returncode}):\n{r.stderr[-2000:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 KDA_WORKLOAD = dict(B=2, H=32, T=8192, C=64, DK=128, DV=128)
@@ -177,6 +179,7 @@ def gdn_config_secondary(B, H, T, dtype_name, h0_std, steps, warmup, kind="gdn")
     dev = torch.device("cuda:0")
     C, DK, DV = 64, 128, 128
     dtype = torch.bfloat16 if dtype_name == "bf16" else torch.float32
+    esize = 2 if dtype_name == "bf16" else 4
     d = make_delta_inputs(B, H, T, DK, DV, kind=kind, dtype=dtype, seed=4, h0_std=h0_std,
                           device=dev)
     o = torch.empty(B, H, T, DV, device=dev, dtype=torch.float32)
@@ -184,20 +187,24 @@ def gdn_config_secondary(B, H, T, dtype_name, h0_std, steps, warmup, kind="gdn")
     ws = gdn_workspace(B, H, T, C, DK, DV, dtype, dev)
     ms = _event_ms(lambda: gdn_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"],
                                              out=o, final_out=hf, workspace=ws), steps, warmup)
-    m = stage_model(B, H, T, C, DK, DV, 2 if dtype_name == "bf16" else 4)
+    m = stage_model(B, H, T, C, DK, DV, esize)
     nbytes = m["chunk_local"]["bytes"] + m["scan_output"]["bytes"] + (
         B * H * DK * DV * 4 if h0_std is not None else 0)
     if kind == "deltanet":      # no gate to read in stage 1 (stage 2 still reads the zero G)
         nbytes -= B * H * T * 4
+    comp = compulsory_bytes(B, H, T, DK, DV, esize, h0=h0_std is not None,
+                            g_channels=0 if kind == "deltanet" else 1)
     flops = m["chunk_local"]["flops"] + m["scan_output"]["flops"]
+    s = ms * 1e-3
     return {"workload": f"{'DeltaNet' if kind == 'deltanet' else 'GDN'} chunked forward B{B} H{H} "
                         f"T{T} C64 dk128 dv128, {dtype_name} in"
                         f"{', h0' if h0_std is not None else ''}, fp32 state/accum/o",
             "B": B, "H": H, "T": T, "dtype": dtype_name, "ms_per_step": round(ms, 5),
-            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "chains": B * H,
+            "tokens_per_s": round(B * T / s, 1), "chains": B * H,
             "chunks_per_chain": T // C, "bytes": nbytes,
-            "hbm_frac": round(nbytes / (ms * 1e-3) / PEAK_HBM, 4),
-            "mfma_frac": round(flops / (ms * 1e-3) / (PEAK_BF16 if dtype_name == "bf16" else PEAK_FP32), 4)}
+            "hbm_frac": round(nbytes / s / PEAK_HBM, 4),
+            "compulsory_bytes": comp, "compulsory_hbm_frac": round(comp / s / PEAK_HBM, 4),
+            "mfma_frac": round(flops / s / (PEAK_BF16 if dtype_name == "bf16" else PEAK_FP32), 4)}
 
 
 def kkt_inverse_secondary(steps, warmup):
@@ -247,10 +254,11 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=50,
-                    help="untimed forwards first (the clock takes a few ms of load to settle)")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--event-steps", type=int, default=30,
+                    help="forwards timed per kernel (HIP events) after the timed loop")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true", help="skip the secondary records")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run three plain device copies of MIB MiB: the "
@@ -265,6 +273,9 @@ def main(argv=None) -> int:
               file=sys.stderr)
         return 2
 
+    # the CPU baseline first: its child process forks workers, which must not inherit a GPU context
+    cpu = None if args.no_cpu_baseline else cpu_baseline(runs=args.cpu_runs)
+
     import torch
     from pto_fuser_amd import _hip
     from pto_fuser_amd.forwards import make_delta_inputs
@@ -277,85 +288,96 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     B, H, T, C, DK, DV = (WORKLOAD[k] for k in ("B", "H", "T", "C", "DK", "DV"))
     dtype = torch.bfloat16
-    inputs = make_delta_inputs(B, H, T, DK, DV, kind="gdn", dtype=dtype, seed=0)
-    d = {n: (None if t is None else t.to(dev)) for n, t in inputs.items()}
+    d = make_delta_inputs(B, H, T, DK, DV, kind="gdn", dtype=dtype, seed=0, device=dev)
     o = torch.empty(B, H, T, DV, device=dev, dtype=torch.float32)
     hf = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32)
     ws = gdn_workspace(B, H, T, C, DK, DV, dtype, dev)
     lib = _hip.load()
+    lib_hash = lib.pf_source_hash().decode()
     code = _hip.PF_DTYPE_BF16
     scale = DK ** -0.5
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     P = {n: _hip.ptr(t) for n, t in d.items()}
 
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record(stream)
+    def stage1():
         st = lib.pf_gdn_chunk_local_exec(P["q"], P["k"], P["beta"], P["g"], B, H, T, C, DK, DV,
                                          code, scale, ws.handle, sh)
         if st:
             _hip.check("pf_gdn_chunk_local_exec", st)
-        if ev is not None:
-            ev[1].record(stream)
+
+    def stage2():
         st = lib.pf_gdn_scan_output_exec(P["q"], P["k"], P["v"], P["beta"], None, _hip.ptr(o),
                                          _hip.ptr(hf), B, H, T, C, DK, DV, code, ws.handle, sh)
         if st:
             _hip.check("pf_gdn_scan_output_exec", st)
-        if ev is not None:
-            ev[2].record(stream)
 
+    def step():
+        stage1()
+        stage2()
+
+    copy_GBps = device_copy_GBps()
     for _ in range(args.warmup):
         step()
-    # per-kernel events on every `stride`-th timed step (about ten samples)
-    stride = max(1, args.steps // 10)
-    events = {i: [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-              for i in range(0, args.steps, stride)}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(events.get(i))
+    for _ in range(args.steps):
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) / args.steps * 1e3
-    k1_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events.values())
-    k2_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in events.values())
+
+    # per-kernel durations: a separate pass, events on the launch stream around each kernel
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.event_steps)]
+    for e in ev:
+        e[0].record(stream)
+        stage1()
+        e[1].record(stream)
+        stage2()
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    k1_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in ev)
+    k2_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev)
 
     model = stage_model(B, H, T, C, DK, DV, esize=2)
+    comp = compulsory_bytes(B, H, T, DK, DV, esize=2)
     stages = {}
     for name, ms in (("chunk_local", k1_ms), ("scan_output", k2_ms)):
         m = model[name]
-        s = ms * 1e-3
+        sec = ms * 1e-3
         stages[name] = {
             "avg_ms": round(ms, 5), "bytes": m["bytes"], "flops": m["flops"],
             "bytes_per_unit": m["bytes_per_unit"], "flops_per_unit": m["flops_per_unit"],
             "units": m["units"],
-            "hbm_GBps": round(m["bytes"] / s / 1e9, 1),
-            "hbm_frac": round(m["bytes"] / s / PEAK_HBM, 4),
-            "mfma_TFLOPs": round(m["flops"] / s / 1e12, 2),
-            "mfma_bf16_frac": round(m["flops"] / s / PEAK_BF16, 4),
+            "hbm_GBps": round(m["bytes"] / sec / 1e9, 1),
+            "hbm_frac": round(m["bytes"] / sec / PEAK_HBM, 4),
+            "mfma_TFLOPs": round(m["flops"] / sec / 1e12, 2),
+            "mfma_bf16_frac": round(m["flops"] / sec / PEAK_BF16, 4),
+            "traffic": measured_traffic(name, lib_hash),
         }
-    dom = max(stages, key=lambda n: stages[n]["avg_ms"])
-    ds = stages[dom]
-    roofline = {"kernel": dom, "bound": "hbm", "achieved": ds["hbm_GBps"],
-                "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": ds["hbm_frac"],
-                "traffic": measured_traffic(dom), "algorithmic_bytes": ds["bytes"]}
-    for name in stages:
-        stages[name]["traffic"] = measured_traffic(name)
-    copy_GBps = device_copy_GBps()
-    roofline["device_copy_GBps"] = round(copy_GBps, 1)
-    roofline["frac_of_device_copy"] = round(ds["hbm_GBps"] / copy_GBps, 4)
+    ds = stages["scan_output"]
+    k2 = k2_ms * 1e-3
+    roofline = {"kernel": "scan_output", "bound": "hbm",
+                "achieved": round(comp / k2 / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                "frac": round(comp / k2 / PEAK_HBM, 4), "traffic": ds["traffic"],
+                "bytes": comp, "bytes_per_unit": comp // model["scan_output"]["units"],
+                "units": model["scan_output"]["units"], "kernel_avg_ms": round(k2_ms, 5),
+                "own_bytes": ds["bytes"], "own_achieved": ds["hbm_GBps"],
+                "own_frac": ds["hbm_frac"],
+                "device_copy_GBps": round(copy_GBps, 1),
+                "frac_of_device_copy": round(comp / k2 / 1e9 / copy_GBps, 4),
+                "source_hash": lib_hash}
     total_bytes = sum(model[n]["bytes"] for n in model)
     total_flops = sum(model[n]["flops"] for n in model)
+    fs = ms_per_step * 1e-3
 
     line = {
         "metric": METRIC,
-        "value": round(B * T / (ms_per_step * 1e-3), 1),
+        "value": round(B * T / fs, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "event_samples": len(events),
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -366,9 +388,11 @@ def main(argv=None) -> int:
                                "fp32 state/accum/o", **WORKLOAD},
         "roofline": roofline,
         "stages": stages,
-        "forward": {"bytes": total_bytes, "flops": total_flops,
-                    "hbm_frac": round(total_bytes / (ms_per_step * 1e-3) / PEAK_HBM, 4),
-                    "mfma_bf16_frac": round(total_flops / (ms_per_step * 1e-3) / PEAK_BF16, 4)},
+        "forward": {"compulsory_bytes": comp, "hbm_frac": round(comp / fs / PEAK_HBM, 4),
+                    "own_bytes": total_bytes, "own_hbm_frac": round(total_bytes / fs / PEAK_HBM, 4),
+                    "flops": total_flops,
+                    "mfma_bf16_frac": round(total_flops / fs / PEAK_BF16, 4),
+                    "event_steps": args.event_steps},
     }
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
@@ -379,7 +403,7 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         line["calibration_copy_bytes"] = n * 4
     if not args.no_secondary:
-        sec_steps, sec_warm = max(1, min(args.steps, 50)), min(args.warmup, 10)
+        sec_steps, sec_warm = max(1, min(args.steps, 50)), min(max(args.warmup, 5), 10)
         line["secondary"] = {
             "kda_config5": kda_secondary(sec_steps, sec_warm),
             "gdn_config4_long_context": gdn_config_secondary(1, 32, 32768, "bf16", 0.02, sec_steps,
@@ -388,8 +412,8 @@ def main(argv=None) -> int:
             "deltanet_config1": gdn_config_secondary(1, 4, 512, "fp32", None, sec_steps,
                                                      sec_warm, kind="deltanet"),
         }
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(inputs, runs=args.cpu_runs)
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
     return 0
 

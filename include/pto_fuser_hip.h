@@ -37,6 +37,10 @@ extern "C" {
 const char* pf_status_string(int status);
 /* ABI revision of this library. */
 int pf_abi_version(void);
+/* Hash of the sources, headers and compiler flags the library was built from (16 hex digits);
+ * the Python loader refuses a library whose hash differs from the source tree's.  No counterpart
+ * in the reference, whose registry recompiles per shape (fused.py:58-77). */
+const char* pf_source_hash(void);
 
 /* ------------------------------------------------------------------------------------------
  * Fused gated delta-rule forward (GDN; DeltaNet when g == NULL).
@@ -116,8 +120,13 @@ int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_o
 int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream);
 
 /* ------------------------------------------------------------------------------------------
- * Stage kernels of the compile stack's fused nodes.  No workspace (the reference's setup /
- * teardown pairs have nothing to hold here).  Supported (C, D): C in {16, 32, 64, 128} (bf16
+ * Stage kernels of the compile stack's fused nodes.  They keep no state between calls, so their
+ * setup functions return NULL and their teardowns accept it; they exist so that a recipe of the
+ * reference's shape (fused.py:119-127: setup_sym / teardown_sym around a persistent runner,
+ * fused.py:93-115) binds them unchanged.  Replace scan_setup / scan_teardown
+ * (scan_lib.cpp:81-88, :99), kkt_setup / kkt_setup_v2 / kkt_teardown
+ * (kkt_fused_lib.cpp:98-104, :115, :119-126) and qkv_setup / qkv_setup_v2 / qkv_teardown
+ * (qkv_fused_lib.cpp:123-130, :143, :147-155).  Supported (C, D): C in {16, 32, 64, 128} (bf16
  * needs C >= 32), D in {64, 128}.
  *
  * Row addressing shared by the gated-qk stage: chunk m = c*H + h of an [nc*C, H, D] token
@@ -131,6 +140,8 @@ int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream);
  *   pro_exec / pro_exec_v2 (prologue_fused_lib.cpp; recipes qk_prologue*, fused.py:293-340).
  *   a, b: dtype, rows of D; g, beta: fp32 [nc*C, H] or NULL (0 / 1); mask: [C,C] fp32 or NULL
  *   (then causal = 1 keeps i >= j, 0 keeps i > j); L: [nc*C, H, C] in out_dtype (fp32 or bf16). */
+void* pf_gated_qk_setup(void);
+void pf_gated_qk_teardown(void* ws);
 int pf_gated_qk_exec(const void* a, const void* b, const float* a_scale, const float* b_scale,
                      const float* g, const float* beta, const float* mask, void* L, int nc, int H,
                      int C, int D, int dtype, int causal, int out_dtype, void* stream);
@@ -141,6 +152,8 @@ int pf_gated_qk_exec(const void* a, const void* b, const float* a_scale, const f
  * qkv_flash_native*, fused.py:353-395) and qkvp_exec* (qkv_prologue_fused_lib.cpp; recipes
  * qkvp_flash_native*, fused.py:411-444).  q, k, v [M,C,D] dtype; scales [M,C,D] fp32 or NULL;
  * g, beta [M,C] fp32 or NULL; o [M,C,D] fp32. */
+void* pf_qkv_flash_setup(void);
+void pf_qkv_flash_teardown(void* ws);
 int pf_qkv_flash_exec(const void* q, const void* k, const void* v, const float* q_scale,
                       const float* k_scale, const float* g, const float* beta, float* o, int M,
                       int C, int D, int dtype, void* stream);
@@ -152,6 +165,8 @@ int pf_qkv_flash_exec(const void* q, const void* k, const void* v, const float* 
  * :143-180; recipe chunk_h_scan, fused.py:168-182), which is fixed to C = D = 128 and starts from
  * zero: here h0 [B,H,D,D] fp32 (or NULL = zero) is accepted.  w, u, k [B,nc,C,H,D] dtype;
  * h_out [B,nc,H,D,D] in out_dtype; final_state [B,H,D,D] fp32 or NULL. */
+void* pf_scan_setup(void);
+void pf_scan_teardown(void* ws);
 int pf_scan_exec(const void* w, const void* u, const void* k, const float* decay,
                  const float* h0, void* h_out, float* final_state, int B, int H, int nc, int C,
                  int D, int dtype, int perdim, int out_dtype, void* stream);

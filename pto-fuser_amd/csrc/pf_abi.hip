@@ -8,6 +8,7 @@
 
 #include "../../include/pto_fuser_hip.h"
 #include "pf_chunk_local.h"
+#include "pf_status.h"
 #include "pf_scan_output.h"
 #include "pf_scan_output_tr.h"
 
@@ -59,13 +60,8 @@ bool gdn_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
          valid_dtype(dtype);
 }
 
-int launch_status() {
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? PF_OK : static_cast<int>(e);
-}
-
 template <typename E>
-int chunk_local_launch(const void* q, const void* k, const float* beta, const float* g,
+void chunk_local_launch(const void* q, const void* k, const float* beta, const float* g,
                        float scale, const GdnWorkspace* ws, size_t M, hipStream_t stream) {
   constexpr int C = 64, DK = 128;
   const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
@@ -85,7 +81,6 @@ int chunk_local_launch(const void* q, const void* k, const float* beta, const fl
   a.p_scale = scale;
   a.scale_out = reinterpret_cast<float*>(base + lay.s_off);
   pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
-  return launch_status();
 }
 
 // CUs of the current device (queried once; 256 on MI355X if the query fails).
@@ -103,7 +98,7 @@ int device_cu_count() {
 }
 
 template <typename E>
-int scan_output_launch(const void* q, const void* k, const void* v, const float* beta,
+void scan_output_launch(const void* q, const void* k, const void* v, const float* beta,
                        const float* h0, float* o, float* h_final, int BH, int NC,
                        const GdnWorkspace* ws, hipStream_t stream) {
   constexpr int C = 64, DK = 128, DV = 128, NWC = 2;
@@ -147,7 +142,6 @@ int scan_output_launch(const void* q, const void* k, const void* v, const float*
     pf::scan_output_kernel<E, C, DK, DV, NWC, 1>
         <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
   }
-  return launch_status();
 }
 
 // Shared host checks of the three GDN entry points.
@@ -175,7 +169,12 @@ const char* pf_status_string(int status) {
   return "unknown status";
 }
 
-int pf_abi_version(void) { return 1; }
+int pf_abi_version(void) { return 2; }
+
+#ifndef PF_SOURCE_HASH
+#define PF_SOURCE_HASH "unknown"
+#endif
+const char* pf_source_hash(void) { return PF_SOURCE_HASH; }
 
 size_t pf_gdn_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype) {
   if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return 0;
@@ -211,8 +210,12 @@ int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, con
   const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
   const size_t M = (size_t)B * H * (T / C);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PF_DTYPE_BF16) return chunk_local_launch<bf16>(q, k, beta, g, scale, w, M, s);
-  return chunk_local_launch<float>(q, k, beta, g, scale, w, M, s);
+  pf::LaunchScope scope;
+  if (dtype == PF_DTYPE_BF16)
+    chunk_local_launch<bf16>(q, k, beta, g, scale, w, M, s);
+  else
+    chunk_local_launch<float>(q, k, beta, g, scale, w, M, s);
+  return scope.status();
 }
 
 int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const float* beta,
@@ -223,9 +226,12 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
   if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
   const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  pf::LaunchScope scope;
   if (dtype == PF_DTYPE_BF16)
-    return scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
-  return scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
+    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
+  else
+    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
+  return scope.status();
 }
 
 int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
@@ -261,16 +267,18 @@ int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_o
   a.p_scale = 1.f;
   a.scale_out = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  pf::LaunchScope scope;
   if (dtype == PF_DTYPE_BF16)
     pf::chunk_local_kernel<bf16, float, 64, 128, false, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(a);
   else
     pf::chunk_local_kernel<float, float, 64, 128, false, true><<<dim3((unsigned)M), dim3(256), 0, s>>>(a);
-  return launch_status();
+  return scope.status();
 }
 
 int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream) {
   if (M <= 0 || !A || !T_out) return PF_ERR_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  pf::LaunchScope scope;
   switch (C) {
     case 16: pf::tri_inv_kernel<16><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
     case 32: pf::tri_inv_kernel<32><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
@@ -279,7 +287,7 @@ int pf_tri_inv_exec(const float* A, float* T_out, int M, int C, void* stream) {
     case 128: pf::tri_inv_kernel<128><<<dim3((unsigned)M), dim3(256), 0, s>>>(A, T_out, M); break;
     default: return PF_ERR_ARG;
   }
-  return launch_status();
+  return scope.status();
 }
 
 }  // extern "C"

@@ -5,15 +5,11 @@
 
 #include "../../include/pto_fuser_hip.h"
 #include "pf_kda.h"
+#include "pf_status.h"
 
 namespace {
 
 using pf::bf16;
-
-int launch_status() {
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? PF_OK : static_cast<int>(e);
-}
 
 constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -100,8 +96,9 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   la.KR = reinterpret_cast<bf16*>(base + lay.k_off);
   la.P = reinterpret_cast<bf16*>(base + lay.p_off);
   la.DEC = reinterpret_cast<float*>(base + lay.d_off);
+  pf::LaunchScope scope;
   pf::kda_local_kernel<KC, KD, KD><<<dim3((unsigned)M), dim3(256), 0, s>>>(la);
-  int st = launch_status();
+  const int st = scope.status();
   if (st != PF_OK) return st;
 
   pf::KdaScanArgs sa{};
@@ -119,7 +116,7 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   constexpr int NLW = 4;
   const unsigned grid = (unsigned)(B * H * (KD / 32));
   pf::kda_scan_kernel<KC, KD, KD, NLW><<<dim3(grid), dim3(64 * (2 + NLW)), 0, s>>>(sa);
-  return launch_status();
+  return scope.status();
 }
 
 }  // extern "C"

@@ -5,15 +5,12 @@
 
 #include "../../include/pto_fuser_hip.h"
 #include "pf_stages.h"
+#include "pf_status.h"
 
 namespace {
 
 using pf::bf16;
 
-int launch_status() {
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? PF_OK : static_cast<int>(e);
-}
 
 // Supported (C, D): C in {16, 32, 64, 128} (bf16 needs C >= 32: one bf16 MFMA contracts 32 rows),
 // D in {64, 128}.
@@ -49,8 +46,9 @@ struct GatedQkLaunch {
   hipStream_t s;
   template <typename E, int C, int D>
   int operator()() {
+    pf::LaunchScope scope;
     pf::gated_qk_kernel<E, C, D><<<dim3(grid), dim3(256), 0, s>>>(a);
-    return launch_status();
+    return scope.status();
   }
 };
 
@@ -60,8 +58,9 @@ struct QkvFlashLaunch {
   hipStream_t s;
   template <typename E, int C, int D>
   int operator()() {
+    pf::LaunchScope scope;
     pf::qkv_flash_kernel<E, C, D><<<dim3(grid), dim3(256), 0, s>>>(a);
-    return launch_status();
+    return scope.status();
   }
 };
 
@@ -73,8 +72,9 @@ struct ScanLaunch {
   int operator()() {
     constexpr int NW = 2;
     const unsigned grid = (unsigned)(BH * (D / (16 * NW)));
+    pf::LaunchScope scope;
     pf::scan_state_kernel<E, C, D, NW><<<dim3(grid), dim3(64 * NW), 0, s>>>(a);
-    return launch_status();
+    return scope.status();
   }
 };
 
@@ -120,5 +120,14 @@ int pf_scan_exec(const void* w, const void* u, const void* k, const float* decay
   l.s = static_cast<hipStream_t>(stream);
   return dispatch(dtype, C, D, l);
 }
+
+// The stage kernels hold no state between calls: setup returns NULL (the recipe's workspace
+// handle) and teardown accepts it, so a recipe that names setup_sym / teardown_sym binds them.
+void* pf_gated_qk_setup(void) { return nullptr; }
+void pf_gated_qk_teardown(void* ws) { (void)ws; }
+void* pf_qkv_flash_setup(void) { return nullptr; }
+void pf_qkv_flash_teardown(void* ws) { (void)ws; }
+void* pf_scan_setup(void) { return nullptr; }
+void pf_scan_teardown(void* ws) { (void)ws; }
 
 }  // extern "C"

@@ -3,11 +3,16 @@
 The library is compiled from ``pto-fuser_amd/csrc/*.hip`` into
 ``pto-fuser_amd/pto_fuser_amd/lib/libptofuser_hip.so``; it travels with the source tree, so a
 GPU box loads the file built here.  ``build()`` always recompiles (it is the "does it build"
-check); ``ensure_built()`` compiles only when the library is missing or older than a source.
+check); ``ensure_built()`` compiles only when no library exists yet.
+
+Every build embeds :func:`source_hash` (the sources, headers and compiler flags it was made
+from) as ``pf_source_hash()``; the loader compares it with the tree's current hash and refuses a
+library built from other sources, so an edit without a rebuild never ships a stale library.
 """
 from __future__ import annotations
 
 import glob
+import hashlib
 import os
 import shutil
 import subprocess
@@ -48,6 +53,19 @@ def headers() -> List[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h")))
 
 
+def source_hash() -> str:
+    """16 hex digits of SHA-256 over every source and header (name and content) and the hipcc
+    flags: what the library's ``pf_source_hash()`` must return for it to be current."""
+    h = hashlib.sha256()
+    for path in sources() + headers():
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+        h.update(b"\0")
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def _run(cmd: List[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -68,23 +86,17 @@ def build(verbose: bool = False, out: Optional[str] = None) -> str:
     srcs = sources()
     objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
     jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", "8"))))
+    tag = f'-DPF_SOURCE_HASH="{source_hash()}"'
     try:
         with ThreadPoolExecutor(jobs) as pool:
-            list(pool.map(lambda so: _run([hipcc, *HIPCC_FLAGS, "-I", INCLUDE, "-c", so[0], "-o", so[1]],
-                                          verbose), zip(srcs, objs)))
+            list(pool.map(lambda so: _run([hipcc, *HIPCC_FLAGS, tag, "-I", INCLUDE, "-c", so[0],
+                                           "-o", so[1]], verbose), zip(srcs, objs)))
         tmp = out + f".tmp{os.getpid()}"
         _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp], verbose)
         os.replace(tmp, out)
     finally:
         shutil.rmtree(obj_dir, ignore_errors=True)
     return out
-
-
-def is_stale(path: str = LIB_PATH) -> bool:
-    if not os.path.exists(path):
-        return True
-    t = os.path.getmtime(path)
-    return any(os.path.getmtime(s) > t for s in sources() + headers())
 
 
 def ensure_built(verbose: bool = False) -> str:

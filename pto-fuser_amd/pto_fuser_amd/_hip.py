@@ -27,6 +27,7 @@ c_void_p, c_int, c_float, c_size_t = ctypes.c_void_p, ctypes.c_int, ctypes.c_flo
 SIGNATURES = {
     "pf_status_string": (ctypes.c_char_p, [c_int]),
     "pf_abi_version": (c_int, []),
+    "pf_source_hash": (ctypes.c_char_p, []),
     "pf_gdn_workspace_bytes": (c_size_t, [c_int] * 7),
     "pf_gdn_setup": (c_void_p, [c_int] * 7),
     "pf_gdn_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
@@ -42,6 +43,12 @@ SIGNATURES = {
     "pf_kda_setup": (c_void_p, [c_int] * 7),
     "pf_kda_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
     "pf_kda_teardown": (None, [c_void_p]),
+    "pf_gated_qk_setup": (c_void_p, []),
+    "pf_gated_qk_teardown": (None, [c_void_p]),
+    "pf_qkv_flash_setup": (c_void_p, []),
+    "pf_qkv_flash_teardown": (None, [c_void_p]),
+    "pf_scan_setup": (c_void_p, []),
+    "pf_scan_teardown": (None, [c_void_p]),
 }
 
 
@@ -60,15 +67,23 @@ def lib_path() -> str:
     return os.environ.get("PF_HIP_LIB", _build.LIB_PATH)
 
 
+class StaleLibraryError(RuntimeError):
+    """The library on disk was built from sources other than the tree's current ones."""
+
+
 def load(build_if_missing: bool = True) -> ctypes.CDLL:
     """Load (once) the HIP library and bind every signature.  Builds it first only when no
-    library file exists yet."""
+    library file exists yet.  The in-tree library must carry the current tree's source hash
+    (``_build.source_hash()``): one built from other sources raises :class:`StaleLibraryError`
+    instead of running old kernels.  ``PF_HIP_LIB`` names another library file and skips the
+    check (for libraries built elsewhere on purpose)."""
     global _LIB
     if _LIB is not None:
         return _LIB
     path = lib_path()
+    explicit = "PF_HIP_LIB" in os.environ
     if not os.path.exists(path):
-        if not build_if_missing or "PF_HIP_LIB" in os.environ:
+        if not build_if_missing or explicit:
             raise FileNotFoundError(f"libptofuser_hip.so not found at {path}")
         _build.ensure_built()
     lib = ctypes.CDLL(path)
@@ -76,6 +91,12 @@ def load(build_if_missing: bool = True) -> ctypes.CDLL:
         fn = getattr(lib, name)          # AttributeError here = ABI drift, loudly
         fn.restype = res
         fn.argtypes = args
+    if not explicit:
+        built, tree = lib.pf_source_hash().decode(), _build.source_hash()
+        if built != tree:
+            raise StaleLibraryError(
+                f"{path} was built from other sources (library {built}, tree {tree}): "
+                f"rebuild it with __graft_entry__.build() before running")
     _LIB = lib
     return lib
 

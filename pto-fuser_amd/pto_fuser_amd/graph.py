@@ -82,7 +82,9 @@ class GraphReplayExecutor:
         torch.cuda.synchronize()
 
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        # captured on the warmup stream: the fused kernels' workspaces are cached per stream
+        # and were allocated there by the warmup (capture itself must not allocate them)
+        with torch.cuda.graph(graph, stream=side):
             with _registry.capture_mode():
                 env = self._exec.run(program, self._static_in, return_env=True)
         torch.cuda.synchronize()

@@ -63,7 +63,6 @@ class GdnWorkspace:
             raise _hip.HipKernelError("pf_gdn_setup", _hip.PF_ERR_ALLOC,
                                       "workspace allocation failed or shape unsupported")
         self.handle = handle
-        self.key = (B, H, T, C, DK, DV, dtype_code, str(device))
         self.bytes = lib.pf_gdn_workspace_bytes(B, H, T, C, DK, DV, dtype_code)
         self._finalizer = weakref.finalize(self, lib.pf_gdn_teardown, handle)
 
@@ -71,17 +70,33 @@ class GdnWorkspace:
         self._finalizer()
 
 
-_WORKSPACES: Dict[tuple, GdnWorkspace] = {}
+_WORKSPACES: Dict[tuple, object] = {}
+
+
+def _stream_key(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _cached_workspace(key: tuple, make):
+    """The workspace cached under ``key`` (shape, device and the current stream), created on
+    first use.  One per stream: forwards of the same shape enqueued on two streams would
+    otherwise overwrite each other's intermediates.  Creating one allocates device memory, which
+    a HIP graph capture must not record: under capture a missing workspace raises (run the call
+    once on the capture stream before capturing, as graph.GraphReplayExecutor's warmup does)."""
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("no workspace for this shape on the capturing stream: run the "
+                               "forward once on that stream before capturing it")
+        ws = make()
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def gdn_workspace(B, H, T, C, DK, DV, dtype: torch.dtype, device) -> GdnWorkspace:
     code = _dtype_code(dtype)
-    key = (B, H, T, C, DK, DV, code, str(device))
-    ws = _WORKSPACES.get(key)
-    if ws is None:
-        ws = GdnWorkspace(B, H, T, C, DK, DV, code, device)
-        _WORKSPACES[key] = ws
-    return ws
+    key = ("gdn", B, H, T, C, DK, DV, code, str(device), _stream_key(device))
+    return _cached_workspace(key, lambda: GdnWorkspace(B, H, T, C, DK, DV, code, device))
 
 
 class KdaWorkspace:
@@ -97,7 +112,6 @@ class KdaWorkspace:
             raise _hip.HipKernelError("pf_kda_setup", _hip.PF_ERR_ALLOC,
                                       "workspace allocation failed or shape unsupported")
         self.handle = handle
-        self.key = ("kda", B, H, T, C, DK, DV, dtype_code, str(device))
         self.bytes = lib.pf_kda_workspace_bytes(B, H, T, C, DK, DV, dtype_code)
         self._finalizer = weakref.finalize(self, lib.pf_kda_teardown, handle)
 
@@ -107,12 +121,8 @@ class KdaWorkspace:
 
 def kda_workspace(B, H, T, C, DK, DV, dtype: torch.dtype, device) -> KdaWorkspace:
     code = _dtype_code(dtype)
-    key = ("kda", B, H, T, C, DK, DV, code, str(device))
-    ws = _WORKSPACES.get(key)
-    if ws is None:
-        ws = KdaWorkspace(B, H, T, C, DK, DV, code, device)
-        _WORKSPACES[key] = ws
-    return ws
+    key = ("kda", B, H, T, C, DK, DV, code, str(device), _stream_key(device))
+    return _cached_workspace(key, lambda: KdaWorkspace(B, H, T, C, DK, DV, code, device))
 
 
 def release_workspaces() -> None:

@@ -1,5 +1,7 @@
 """bench.py's host-side pieces on the CPU: the algorithmic byte / flop models behind `roofline`,
-the recorded counter traffic, and the one-GPU contract (--gpus N > 1 exits with a message)."""
+the recorded counter traffic, the CPU baseline child and the one-GPU contract (--gpus N > 1 exits
+with a message)."""
+import json
 import subprocess
 import sys
 
@@ -30,15 +32,54 @@ def test_stage_model_per_chunk_bytes_and_flops():
     assert f["scan_output"]["bytes_per_unit"] - s2["bytes_per_unit"] == (2 * C * DK + C * DV + 2 * C * C) * 2
 
 
-def test_measured_traffic_matches_the_byte_model():
-    """The counter figures recorded in bench.py (FETCH x2, WRITE x1) agree with the algorithmic
-    bytes of the headline launch to within 0.2 %: neither kernel re-reads."""
+def test_compulsory_bytes_of_the_headline():
+    """q, k, v bf16 + beta, g fp32 in; o fp32 and the final state out: 341.8 MB, i.e. 83 456 B per
+    64-token chunk (82 432 B of token data + 1/64 of the chain's 64 KiB final state)."""
+    comp = bench.compulsory_bytes(4, 16, 4096, DK, DV, 2)
+    assert comp == 341_835_776
+    assert comp == 4096 * (3 * C * 128 * 2 + 2 * C * 4 + C * DV * 4) + 64 * DK * DV * 4
+    assert bench.compulsory_bytes(1, 32, 32768, DK, DV, 2, h0=True) == 1_354_760_192
+    # KDA: g holds DK values per token
+    assert bench.compulsory_bytes(2, 32, 8192, DK, DV, 2, g_channels=DK) == \
+        bench.kda_model(2, 32, 8192, C, DK, DV)["compulsory_bytes"]
+
+
+def test_measured_traffic_keyed_to_the_source_hash(tmp_path, monkeypatch):
+    """Counter traffic is the recorded FETCH_SIZE / WRITE_SIZE KiB scaled by the copy factors, and
+    only for the build it was recorded from: another source hash gives None."""
+    rec = {"source_hash": "abc", "scale": {"FETCH_SIZE": 2.0, "WRITE_SIZE": 1.0},
+           "kernels": {"scan_output": {"FETCH_SIZE": 100.0, "WRITE_SIZE": 50.0}}}
+    path = tmp_path / "c.json"
+    path.write_text(json.dumps(rec))
+    monkeypatch.setattr(bench, "COUNTERS", str(path))
+    assert bench.measured_traffic("scan_output", "abc") == (200 + 50) * 1024
+    assert bench.measured_traffic("scan_output", "def") is None
+    assert bench.measured_traffic("no_such_kernel", "abc") is None
+    monkeypatch.setattr(bench, "COUNTERS", str(tmp_path / "missing.json"))
+    assert bench.measured_traffic("scan_output", "abc") is None
+
+
+def test_recorded_counters_match_the_byte_model():
+    """The committed counter record (whatever build it belongs to) agrees with the algorithmic
+    bytes of its kernels to within 0.5 %: neither kernel re-reads."""
+    with open(bench.COUNTERS) as f:
+        rec = json.load(f)
     m = bench.stage_model(4, 16, 4096, C, DK, DV, 2)
-    for k in ("chunk_local", "scan_output"):
-        traffic = bench.measured_traffic(k)
-        assert traffic is not None
-        assert abs(traffic / m[k]["bytes"] - 1) < 2e-3, (k, traffic, m[k]["bytes"])
-    assert bench.measured_traffic("no_such_kernel") is None
+    for k, kib in rec["kernels"].items():
+        traffic = sum(kib[c] * rec["scale"][c] * 1024 for c in ("FETCH_SIZE", "WRITE_SIZE"))
+        assert abs(traffic / rec["model_bytes"][k] - 1) < 5e-3, (k, traffic)
+        if k in m:
+            assert rec["model_bytes"][k] == m[k]["bytes"], k
+
+
+def test_cpu_baseline_child_reports_cores():
+    r = subprocess.run([sys.executable, "-m", "oracle.cpu_baseline", "--B", "1", "--H", "2",
+                        "--T", "128", "--runs", "1", "--workers", "2"], capture_output=True,
+                       text=True, cwd=bench.ROOT, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    assert d["cores"] == 2 and d["kind"] == "port" and d["unit"] == "tokens/s"
+    assert d["value"] > 0 and d["single_core_value"] > 0 and d["host_cpus"] >= 1
 
 
 def test_kda_model():

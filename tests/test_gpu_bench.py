@@ -32,7 +32,11 @@ def test_bench_json_contract():
     rf = d["roofline"]
     assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["peak"] == 8000.0
     assert 0 < rf["frac"] < 1 and abs(rf["frac"] - rf["achieved"] / rf["peak"]) < 1e-3
-    assert rf["traffic"] is not None and rf["device_copy_GBps"] > 0
+    # achieved = the forward's compulsory bytes over the dominant kernel's event-timed duration
+    assert rf["bytes"] == bench.compulsory_bytes(4, 16, 4096, 128, 128, 2)
+    assert abs(rf["achieved"] - rf["bytes"] / (rf["kernel_avg_ms"] * 1e-3) / 1e9) / rf["achieved"] < 1e-3
+    assert rf["traffic"] is None or rf["traffic"] > 0
+    assert rf["device_copy_GBps"] > 0
     assert set(d["stages"]) == {"chunk_local", "scan_output"}
     assert set(d["secondary"]) == {"kda_config5", "gdn_config4_long_context",
                                    "kkt_inverse_config3", "deltanet_config1"}

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, record_error
 from oracle.gdn_oracle import (deltanet_reference, gdn_reference, max_abs, max_rel,
                                tri_inv_reference, within_chunk_cumsum)
 from pto_fuser_amd import gdn_chunk_forward, kkt_inverse, tri_inv
@@ -30,6 +30,16 @@ def _run(inp):
     return o.cpu().numpy(), h.cpu().numpy()
 
 
+def _check(case, o, h, o_ref, h_ref, bf16):
+    """The bound of the north star: bf16 inputs max abs <= 2e-2, fp32 max rel <= 1e-4, on o and
+    the final state; every comparison's magnitudes are recorded for the session summary."""
+    tol = f"max abs <= {BF16_TOL}" if bf16 else f"max rel <= {FP32_TOL}"
+    for name, got, ref in (("o", o, o_ref), ("h", h, h_ref)):
+        e = record_error(case, name, got, ref, tol)
+        err = e["abs"] if bf16 else e["rel"]
+        assert err <= (BF16_TOL if bf16 else FP32_TOL), (case, name, e)
+
+
 def _oracle(inp, dtype=np.float64):
     x = as_oracle_inputs(inp)
     g = x["g"] if x["g"] is not None else np.zeros(x["beta"].shape)
@@ -45,7 +55,8 @@ def test_tri_inv_matches_oracle(C):
     A += np.triu(np.ones((C, C), np.float32), 1) * 7.0      # so must the upper triangle
     got = tri_inv(torch.from_numpy(A).to(DEV)).cpu().numpy()
     ref = tri_inv_reference(np.tril(A, -1))
-    assert max_rel(got, ref) <= FP32_TOL, max_rel(got, ref)
+    e = record_error(f"tri_inv C={C} M=96", "T", got, ref, f"max rel <= {FP32_TOL}")
+    assert e["rel"] <= FP32_TOL, e
     assert np.all(np.triu(got, 1) == 0) and np.all(got[:, np.arange(C), np.arange(C)] == 1)
 
 
@@ -67,8 +78,10 @@ def test_kkt_inverse_config3(dtype):
     A_ref = np.tril(kk @ kk.transpose(0, 2, 1) * np.where(dG <= 0, np.exp(np.minimum(dG, 0)), 0)
                     * bt[:, :, None], -1)
     T_ref = tri_inv_reference(A_ref)
-    assert max_rel(A.cpu().numpy(), A_ref) <= FP32_TOL
-    assert max_rel(Tm.cpu().numpy(), T_ref) <= FP32_TOL, max_rel(Tm.cpu().numpy(), T_ref)
+    case = f"kkt+inverse config 3 {str(dtype).replace('torch.', '')}"
+    ea = record_error(case, "A", A.cpu().numpy(), A_ref, f"max rel <= {FP32_TOL}")
+    et = record_error(case, "T", Tm.cpu().numpy(), T_ref, f"max rel <= {FP32_TOL}")
+    assert ea["rel"] <= FP32_TOL and et["rel"] <= FP32_TOL, (ea, et)
 
 
 def test_deltanet_fp32_config1():
@@ -77,8 +90,8 @@ def test_deltanet_fp32_config1():
     o, h = _run(inp)
     x = as_oracle_inputs(inp)
     ref = deltanet_reference(x["q"], x["k"], x["v"], x["beta"], C=64, dtype=np.float64)
-    assert max_rel(o, ref["o"].reshape(o.shape)) <= FP32_TOL
-    assert max_rel(h, ref["final"]) <= FP32_TOL
+    _check("DeltaNet fp32 config 1 B1 H4 T512", o, h, ref["o"].reshape(o.shape), ref["final"],
+           bf16=False)
 
 
 @pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 256), (1, 8, 1024)])
@@ -87,8 +100,20 @@ def test_gdn_fp32_with_h0(B, H, T):
     inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.float32, seed=B * 100 + H, h0_std=0.02)
     o, h = _run(inp)
     o_ref, h_ref = _oracle(inp)
-    assert max_rel(o, o_ref) <= FP32_TOL, max_rel(o, o_ref)
-    assert max_rel(h, h_ref) <= FP32_TOL, max_rel(h, h_ref)
+    _check(f"GDN fp32 B{B} H{H} T{T} h0", o, h, o_ref, h_ref, bf16=False)
+
+
+@pytest.mark.parametrize("B,H,T,h0", [(1, 3, 64, False), (2, 2, 64, True), (1, 4, 128, True),
+                                      (1, 2, 192, False)])
+def test_gdn_bf16_short_sequences(B, H, T, h0):
+    """bf16 at one, two and three chunks per chain: T = C takes the single-chunk path of the
+    scan launcher, T = 2C and 3C the shortest runs of the pipelined kernel."""
+    announce(f"GDN bf16 B{B} H{H} T{T} h0={h0}")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.bfloat16, seed=T + B * 10 + H,
+                            h0_std=0.02 if h0 else None)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    _check(f"GDN bf16 B{B} H{H} T{T}{' h0' if h0 else ''}", o, h, o_ref, h_ref, bf16=True)
 
 
 def test_gdn_bf16_config2():
@@ -96,8 +121,7 @@ def test_gdn_bf16_config2():
     inp = make_delta_inputs(4, 16, 4096, kind="gdn", dtype=torch.bfloat16, seed=0)
     o, h = _run(inp)
     o_ref, h_ref = _oracle(inp, dtype=np.float32)
-    assert max_abs(o, o_ref) <= BF16_TOL, max_abs(o, o_ref)
-    assert max_abs(h, h_ref) <= BF16_TOL, max_abs(h, h_ref)
+    _check("GDN bf16 config 2 B4 H16 T4096", o, h, o_ref, h_ref, bf16=True)
 
 
 def test_gdn_bf16_config4_long_context():
@@ -105,8 +129,9 @@ def test_gdn_bf16_config4_long_context():
     inp = make_delta_inputs(1, 32, 32768, kind="gdn", dtype=torch.bfloat16, seed=4, h0_std=0.02)
     o, h = _run(inp)
     o_ref, h_ref = _oracle(inp, dtype=np.float32)
-    assert max_abs(o, o_ref) <= BF16_TOL, max_abs(o, o_ref)
-    assert max_abs(h, h_ref) <= BF16_TOL, max_abs(h, h_ref)
+    _check("GDN bf16 config 4 B1 H32 T32768 h0", o, h, o_ref, h_ref, bf16=True)
+    # the state carries 512 chunks of bf16 operand rounding: keep 2x headroom under the bound
+    assert max_abs(h, h_ref) <= BF16_TOL / 2, max_abs(h, h_ref)
 
 
 def test_gdn_deterministic():
@@ -135,8 +160,10 @@ def test_gdn_state_passing_config4():
     o2, h2 = gdn_chunk_forward(second["q"], second["k"], second["v"], second["beta"],
                                second["g"], h0=h1)
     torch.cuda.synchronize()
-    err_o = max_abs(torch.cat([o1, o2], 2).cpu().numpy(), o.cpu().numpy())
-    err_h = max_abs(h2.cpu().numpy(), h.cpu().numpy())
+    err_o = record_error("GDN state passing config 4", "o", torch.cat([o1, o2], 2).cpu().numpy(),
+                         o.cpu().numpy(), "max abs <= 5e-3")["abs"]
+    err_h = record_error("GDN state passing config 4", "h", h2.cpu().numpy(), h.cpu().numpy(),
+                         "max abs <= 5e-3")["abs"]
     assert err_o <= 5e-3 and err_h <= 5e-3, (err_o, err_h)
 
 

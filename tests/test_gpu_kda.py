@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, record_error
 from oracle.gdn_oracle import kda_reference, max_abs
 from pto_fuser_amd import kda_chunk_forward
 from pto_fuser_amd.forwards import as_oracle_inputs, make_delta_inputs
@@ -27,6 +27,12 @@ def _run(inp):
     return o.cpu().numpy(), h.cpu().numpy()
 
 
+def _check(case, o, h, o_ref, h_ref):
+    for name, got, ref in (("o", o, o_ref), ("h", h, h_ref)):
+        e = record_error(case, name, got, ref, f"max abs <= {BF16_TOL}")
+        assert e["abs"] <= BF16_TOL, (case, name, e)
+
+
 def _oracle(inp, dtype=np.float64):
     x = as_oracle_inputs(inp)
     return kda_reference(x["q"], x["k"], x["v"], x["beta"], x["g"], C=64, h0=x["h0"], dtype=dtype)
@@ -40,8 +46,7 @@ def test_kda_bf16_matches_oracle(B, H, T, h0):
                             h0_std=0.02 if h0 else None)
     o, h = _run(inp)
     o_ref, h_ref = _oracle(inp)
-    assert max_abs(o, o_ref) <= BF16_TOL, max_abs(o, o_ref)
-    assert max_abs(h, h_ref) <= BF16_TOL, max_abs(h, h_ref)
+    _check(f"KDA bf16 B{B} H{H} T{T}{' h0' if h0 else ''}", o, h, o_ref, h_ref)
 
 
 def test_kda_bf16_strong_decay():
@@ -51,8 +56,7 @@ def test_kda_bf16_strong_decay():
     inp = make_delta_inputs(1, 2, 512, kind="kda", dtype=torch.bfloat16, seed=11, gate_scale=0.3)
     o, h = _run(inp)
     o_ref, h_ref = _oracle(inp)
-    assert max_abs(o, o_ref) <= BF16_TOL, max_abs(o, o_ref)
-    assert max_abs(h, h_ref) <= BF16_TOL, max_abs(h, h_ref)
+    _check("KDA bf16 B1 H2 T512 strong decay", o, h, o_ref, h_ref)
 
 
 def test_kda_bf16_config5():
@@ -60,8 +64,7 @@ def test_kda_bf16_config5():
     inp = make_delta_inputs(2, 32, 8192, kind="kda", dtype=torch.bfloat16, seed=5)
     o, h = _run(inp)
     o_ref, h_ref = _oracle(inp, dtype=np.float32)
-    assert max_abs(o, o_ref) <= BF16_TOL, max_abs(o, o_ref)
-    assert max_abs(h, h_ref) <= BF16_TOL, max_abs(h, h_ref)
+    _check("KDA bf16 config 5 B2 H32 T8192", o, h, o_ref, h_ref)
 
 
 def test_kda_state_passing():
@@ -75,8 +78,11 @@ def test_kda_state_passing():
     o1, h1 = kda_chunk_forward(half["q"], half["k"], half["v"], half["beta"], half["g"])
     o2, h2 = kda_chunk_forward(rest["q"], rest["k"], rest["v"], rest["beta"], rest["g"], h0=h1)
     torch.cuda.synchronize()
-    assert max_abs(torch.cat([o1, o2], 2).cpu().numpy(), o.cpu().numpy()) <= 1e-3
-    assert max_abs(h2.cpu().numpy(), h.cpu().numpy()) <= 1e-3
+    eo = record_error("KDA state passing B1 H4 T1024", "o", torch.cat([o1, o2], 2).cpu().numpy(),
+                      o.cpu().numpy(), "max abs <= 1e-3")
+    eh = record_error("KDA state passing B1 H4 T1024", "h", h2.cpu().numpy(), h.cpu().numpy(),
+                      "max abs <= 1e-3")
+    assert eo["abs"] <= 1e-3 and eh["abs"] <= 1e-3, (eo, eh)
 
 
 def test_kda_deterministic():
