@@ -10,20 +10,14 @@
 #include "pf_chunk_local.h"
 #include "pf_status.h"
 #include "pf_scan_output.h"
-#include "pf_scan_output_tr.h"
+#include "pf_scan_split.h"
 
-#ifndef PF_TR_LOADER_WAVES
-#define PF_TR_LOADER_WAVES 4
+// loader waves of the split scan kernel for 32-column and for 16-column slices
+#ifndef PF_SPLIT_LW
+#define PF_SPLIT_LW 4
 #endif
-// loader waves of the 16-column variant (one compute wave): two are faster there (long-context
-// GDN, B1 H32 T32768: 0.861 vs 0.896 ms), four for the 32-column kernel (headline: 0.159 vs
-// 0.168 ms)
-#ifndef PF_TR16_LOADER_WAVES
-#define PF_TR16_LOADER_WAVES 2
-#endif
-// compute waves of the bf16 scan kernel; each owns 2 / PF_TR_COMPUTE_WAVES blocks of 16 columns
-#ifndef PF_TR_COMPUTE_WAVES
-#define PF_TR_COMPUTE_WAVES 2
+#ifndef PF_SPLIT16_LW
+#define PF_SPLIT16_LW 4
 #endif
 
 namespace {
@@ -119,26 +113,19 @@ void scan_output_launch(const void* q, const void* k, const void* v, const float
   a.BH = BH;
   a.NC = NC;
   a.scale = reinterpret_cast<const float*>(base + lay.s_off);
-  const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
   if constexpr (std::is_same<E, bf16>::value) {
-    // bf16: row-major staging read back through LDS transpose loads (gfx950); its loader
-    // pipeline assumes at least two chunks per chain, a single chunk takes the generic kernel.
-    // One workgroup per (chain, 32-column slice) and CU; when that leaves CUs idle (fewer than
-    // 8 chains per 32 CUs: long sequences at small batch) the slices are 16 columns wide, one
-    // compute wave each, so twice the workgroups run the same chains.
-    constexpr int NLW = PF_TR_LOADER_WAVES, NLW16 = PF_TR16_LOADER_WAVES;
-    constexpr int NWT = PF_TR_COMPUTE_WAVES, NCB = 2 / NWT;
-    static_assert(NWT * NCB == 2, "the bf16 scan kernel covers 32 state columns per workgroup");
-    if (NC >= 2 && (size_t)BH * (DV / 32) < (size_t)device_cu_count())
-      pf::scan_output_tr_kernel<C, DK, DV, 1, NLW16, 1>
-          <<<dim3((unsigned)(BH * (DV / 16))), dim3(64 * (1 + NLW16)), 0, stream>>>(a);
-    else if (NC >= 2)
-      pf::scan_output_tr_kernel<C, DK, DV, NWT, NLW, NCB><<<dim3(grid), dim3(64 * (NWT + NLW)), 0, stream>>>(a);
+    // bf16: one workgroup per (chain, 32-column slice), or 16-column slices when 32 would leave
+    // CUs idle (fewer than 8 chains per 32 CUs: long sequences at small batch); four MFMA waves
+    // split every chunk (pf_scan_split.h)
+    if ((size_t)BH * (DV / 32) < (size_t)device_cu_count())
+      pf::scan_split_kernel<C, DK, DV, 1, PF_SPLIT16_LW>
+          <<<dim3((unsigned)(BH * (DV / 16))), dim3(64 * (4 + PF_SPLIT16_LW)), 0, stream>>>(a);
     else
-      pf::scan_output_kernel<E, C, DK, DV, NWC, 1>
-          <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
+      pf::scan_split_kernel<C, DK, DV, 2, PF_SPLIT_LW>
+          <<<dim3((unsigned)(BH * (DV / 32))), dim3(64 * (4 + PF_SPLIT_LW)), 0, stream>>>(a);
   } else {
     // fp32: transposed tiles staged by the loader; one LDS buffer (the images are 143 KB)
+    const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
     pf::scan_output_kernel<E, C, DK, DV, NWC, 1>
         <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
   }

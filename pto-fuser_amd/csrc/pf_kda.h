@@ -18,12 +18,14 @@
 //   Y = W S,  v_new = U - Y,  o^T = v_new^T P^T + (QE S)^T,  S <- e^{G_last} (.) S + KR^T v_new
 //
 // so its chunk images hold the already-gated operands and the per-channel decay is one multiply
-// of the state rows per chunk.  The workgroup organisation, the LDS swizzles, the loader pipeline
-// and the LDS-staged output are those of the GDN scan kernel (pf_scan_output_tr.h).
+// of the state rows per chunk.  Two compute waves each hold 16 state columns through the whole
+// chain; four loader waves keep three chunks in flight in registers, write each chunk into the
+// free half of a double-buffered LDS stage (swizzled rows, 16-byte stores) and store the o tiles
+// the compute waves stage in LDS.
 #pragma once
 
 #include "pf_chunk_local.h"
-#include "pf_scan_output_tr.h"
+#include "pf_gfx950.h"
 
 namespace pf {
 

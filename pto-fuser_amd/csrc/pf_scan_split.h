@@ -1,0 +1,420 @@
+// Stage 2 for bf16 operands on gfx950: the state scan fused with the output stage, with every
+// chunk's work split over four MFMA waves (one per SIMD) by token block and state row block.
+//
+// Workgroup = one chain bh x one slice of NCOL = 16*NT state columns.  Per chunk c (C = 64, DK =
+// 128), with T = (I+A)^-1, the pre-scaled causal score P and G from stage 1:
+//
+//   Y = k S,  r = beta v - beta e^G Y,  v_new = T r,
+//   o = scale e^G (q S) + P v_new,  S <- e^{G_last} S + k^T (v_new e^{G_last - G}).
+//
+// Compute wave w (w = 0..3) owns tokens 16w..16w+15 of every chunk (its rows of Y, q S, r, v_new
+// and o) and state rows 32w..32w+31 (fp32, MFMA D layout, for the whole chain).  The products
+// that contract over what another wave owns go through small LDS exchange tiles in the MFMA
+// operand layout, one 16-byte slot per lane, so every exchange read is one contiguous 1 KiB
+// ds_read_b128 per fragment:
+//
+//   SB  the bf16 state, [4 row blocks][NT][64 lanes]: each wave publishes its 32 rows after the
+//       update (its two 16-row D blocks are exactly one permuted-K B fragment), every wave reads
+//       all four as the B operand of k S and the A operand of (q S)^T;
+//   RX  r in bf16, [2 token blocks of 32][NT][64 lanes]: wave w fills half (w & 1) of block
+//       w >> 1 (its D registers are the lane's permuted-K half); wave w reads blocks 0..w>>1 for
+//       v_new = T r (T is lower triangular);
+//   VX  v_new in bf16, the A operand of o^T = v_new^T P^T (causal: blocks 0..w>>1);
+//   VXs v_new e^{G_last - G} / f in bf16, the B operand of the state update (both blocks).
+//
+// Three workgroup barriers per chunk: after RX is written (B1), after VX / VXs (B2), after the
+// state is published and the chunk's stage buffer released (B3).  Per wave and chunk: 16 MFMAs
+// for k S and q S, 2 or 4 for T r, 2 or 4 for P v_new, 8 for the update (NT = 2) — against 64
+// for one wave holding 16 columns through the whole chain.
+//
+// NLW loader waves (the rest of the workgroup) own the loads: chunk c+3's loads issued while the
+// compute waves work on chunk c (three rotating register sets), and chunk c+1 written into the
+// free half of a double-buffered LDS stage (k and q rows swizzled for the permuted-K operand
+// reads and the transposed k^T reads, T and P rows, the v tile row-major, per-token gate tables).
+// Both are spread over the three phases of the interval (k and q loads and k's LDS rows in the
+// first, T and P in the second, v, the gates and q's rows in the third), and the loader waves run
+// at the default wave priority: a burst of loads or LDS writes issued at once, or at a raised
+// priority, was measured to stall the compute waves sharing the SIMDs (one phase lost up to
+// 1 000 cycles).  The compute waves store their o rows themselves, one 16-byte store per lane and
+// column block.  The loaders also carry the deferred state decay: the compute waves hold
+// S~ = S / f with a running factor f folded into the gate tables, and multiply it back only when
+// the loader flags a renormalisation (f below e^-60, or the last chunk, so the final state is
+// exact).
+#pragma once
+
+#include "pf_gfx950.h"
+
+namespace pf {
+
+// LDS image of one chunk.
+template <int C, int DK, int NCOL>
+struct SplitStage {
+  static constexpr int KP = DK + 16;   // k, q rows: Swz<2,3>
+  static constexpr int TP = C + 8;     // T, P rows: Swz<3,1>
+  static constexpr int VP = NCOL + 8;  // v tile rows (bf16, row-major)
+  bf16 ks[C * KP];
+  bf16 qs[C * KP];
+  bf16 ts[C * TP];
+  bf16 ps[C * TP];
+  bf16 vs[C * VP];
+  float BT[C];    // beta_t
+  float BEG[C];   // beta_t e^{G_t} f_c
+  float EGS[C];   // scale e^{G_t} f_c
+  float EL[C];    // e^{G_last - G_t} / f_{c+1}
+  float DL[4];    // [0] factor for the state at this chunk's update, [1] nonzero: apply it
+};
+
+// Loader register image of one chunk (k, q: 1024 16-byte vectors; T, P: 512; v: 8 NCOL).
+template <int NLW, int NCOL>
+struct SplitRegs {
+  static constexpr int NK = 1024 / (64 * NLW), NTP = 512 / (64 * NLW);
+  static constexpr int NV = (8 * NCOL + 64 * NLW - 1) / (64 * NLW);
+  uint4 k[NK], q[NK], t[NTP], p[NTP], v[NV];
+  float g, b;
+};
+
+template <int C, int DK, int DV, int NT, int NLW>
+__global__ __launch_bounds__(64 * (4 + NLW)) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void scan_split_kernel(ScanOutArgs a) {
+  constexpr int NCOL = 16 * NT;
+  using Stage = SplitStage<C, DK, NCOL>;
+  using Regs = SplitRegs<NLW, NCOL>;
+  constexpr int KP = Stage::KP, TP = Stage::TP, VP = Stage::VP;
+  constexpr int NS = DV / NCOL;                 // slices per chain
+  constexpr int FRAG = 64 * 8;                  // bf16 elements of one operand fragment
+  static_assert(C == 64 && DK == 128 && (NT == 1 || NT == 2) && (NLW == 2 || NLW == 4),
+                "tile shapes of the split scan kernel: C 64, DK 128, 16 or 32 columns");
+
+  __shared__ __attribute__((aligned(16))) Stage st[2];
+  __shared__ __attribute__((aligned(16))) bf16 SB[4 * NT * FRAG];
+  __shared__ __attribute__((aligned(16))) bf16 RX[2 * NT * FRAG];
+  __shared__ __attribute__((aligned(16))) bf16 VX[2 * NT * FRAG];
+  __shared__ __attribute__((aligned(16))) bf16 VXs[2 * NT * FRAG];
+
+  int bh, slice;
+  const int bid = blockIdx.x;
+  if (a.BH % 8 == 0) {  // the slices of one chain share an XCD (dispatch is round-robin on XCDs)
+    const int grp = bid / (8 * NS), within = bid % (8 * NS);
+    bh = grp * 8 + (within % 8);
+    slice = within / 8;
+  } else {
+    bh = bid / NS;
+    slice = bid % NS;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
+  const int NC = a.NC;
+  const int col0 = slice * NCOL;
+  const uint32_t Tlen = (uint32_t)NC * C;
+
+  if (w >= 4) {
+    // =========================== loader waves ===========================
+    const int lt = tid - 256;                            // 0 .. 64*NLW-1
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(static_cast<const bf16*>(a.k) + (size_t)bh * Tlen * DK, Tlen * DK * 2);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(static_cast<const bf16*>(a.q) + (size_t)bh * Tlen * DK, Tlen * DK * 2);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(static_cast<const bf16*>(a.v) + (size_t)bh * Tlen * DV, Tlen * DV * 2);
+    const __amdgpu_buffer_rsrc_t rt = make_rsrc(static_cast<const bf16*>(a.Tm) + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(static_cast<const bf16*>(a.P) + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
+    const float* Gc = a.G + (size_t)bh * Tlen;
+    const float* Bc = a.beta + (size_t)bh * Tlen;
+    const float oscale = *a.scale;
+    // k / q rows (16 vectors of 8 per row): vec = lt & 15, a = lt >> 4; the vector index i
+    // supplies the row bits that decide the swizzle's half swap, so the swap is compile-time
+    //   NLW 2: row = a0 | a1<<1 | i0<<2 | a2<<3 | i1<<4 | i2<<5
+    //   NLW 4: row = a0 | a1<<1 | i0<<2 | a2<<3 | a3<<4 | i1<<5
+    const int ka = lt >> 4, kvec = lt & 15;
+    const int krow_l = (ka & 3) | (((ka >> 2) & 1) << 3) | (NLW == 4 ? ((ka >> 3) << 4) : 0);
+    const uint32_t kq_voff = (uint32_t)(krow_l * DK + kvec * 8) * 2;
+    const int kq_lds = krow_l * KP + 8 * (kvec ^ ((ka >> 2) & 1));   // Swz<2,3>: slot ^= row bit 3
+    auto krow_i = [](int i) -> int {
+      return NLW == 2 ? ((i & 1) << 2) | (((i >> 1) & 1) << 4) | (((i >> 2) & 1) << 5)
+                      : ((i & 1) << 2) | (((i >> 1) & 1) << 5);
+    };
+    // T / P rows (8 vectors per row): vec = lt & 7, a = lt >> 3
+    //   NLW 2: row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | i1<<5
+    //   NLW 4: row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | a4<<5
+    const int ta = lt >> 3, tvec = lt & 7;
+    const int trow_l = (ta & 7) | ((ta >> 3) << 4);
+    const uint32_t tp_voff = (uint32_t)(trow_l * C + tvec * 8) * 2;
+    const int tp_lds = trow_l * TP + 8 * tvec;
+    auto trow_i = [](int i) -> int { return NLW == 2 ? ((i & 1) << 3) | (((i >> 1) & 1) << 5) : ((i & 1) << 3); };
+    // v tile (NCOL / 8 vectors per row): vector u = lt + 64 NLW i; lanes past the tile's vectors
+    // repeat one (load only)
+    constexpr int VPR = NCOL / 8, V_VECS = C * VPR, VSTEP = 64 * NLW / VPR;
+    const int vu = lt % V_VECS;
+    const bool v_owner = V_VECS >= 64 * NLW || lt < V_VECS;
+    const int vrow_l = vu / VPR, vvec = vu % VPR;
+    const uint32_t v_voff = (uint32_t)(vrow_l * DV + col0 + vvec * 8) * 2;
+    float Lrun = 0.f;                                   // log of the state factor f_c
+
+    auto load_kq = [&](Regs& r, int ch) {
+      const uint32_t kq_s = (uint32_t)ch * C * DK * 2;
+#pragma unroll
+      for (int i = 0; i < Regs::NK; ++i) {
+        const uint32_t rowi = krow_i(i);
+        r.k[i] = buf_load16(rk, kq_voff, kq_s + rowi * DK * 2);
+        r.q[i] = buf_load16(rq, kq_voff, kq_s + rowi * DK * 2);
+      }
+    };
+    auto load_tp = [&](Regs& r, int ch) {
+      const uint32_t tp_s = (uint32_t)ch * C * C * 2;
+#pragma unroll
+      for (int i = 0; i < Regs::NTP; ++i) {
+        const uint32_t rowi = trow_i(i);
+        r.t[i] = buf_load16(rt, tp_voff, tp_s + rowi * C * 2);
+        r.p[i] = buf_load16(rp, tp_voff, tp_s + rowi * C * 2);
+      }
+    };
+    auto load_vg = [&](Regs& r, int ch) {
+      const uint32_t v_s = (uint32_t)ch * C * DV * 2;
+#pragma unroll
+      for (int i = 0; i < Regs::NV; ++i)
+        r.v[i] = buf_load16(rv, v_voff, v_s + (uint32_t)(VSTEP * i) * DV * 2);
+      // every lane loads (lanes past the first loader wave repeat its rows): no branch around a
+      // load, so the compiler's wait counts stay exact
+      r.g = Gc[(size_t)ch * C + (lt & (C - 1))];
+      r.b = Bc[(size_t)ch * C + (lt & (C - 1))];
+    };
+    auto store_k = [&](Stage& s, const Regs& r) {       // halves already in swizzled order
+#pragma unroll
+      for (int i = 0; i < Regs::NK; ++i) put16(s.ks + kq_lds + krow_i(i) * KP, r.k[i], (i & 1) != 0);
+    };
+    auto store_q = [&](Stage& s, const Regs& r) {
+#pragma unroll
+      for (int i = 0; i < Regs::NK; ++i) put16(s.qs + kq_lds + krow_i(i) * KP, r.q[i], (i & 1) != 0);
+    };
+    auto store_tp = [&](Stage& s, const Regs& r) {
+#pragma unroll
+      for (int i = 0; i < Regs::NTP; ++i) {
+        const int rowi = trow_i(i);
+        put16(s.ts + tp_lds + rowi * TP, r.t[i], (i & 1) != 0);
+        put16(s.ps + tp_lds + rowi * TP, r.p[i], (i & 1) != 0);
+      }
+    };
+    auto store_vg = [&](Stage& s, const Regs& r, int ch) {
+      if (v_owner) {
+#pragma unroll
+        for (int i = 0; i < Regs::NV; ++i)
+          *reinterpret_cast<uint4*>(s.vs + (vrow_l + VSTEP * i) * VP + vvec * 8) = r.v[i];
+      }
+      // gate tables with the deferred state factor f_c = e^{Lrun}
+      const float gl = __shfl(r.g, C - 1);                // G_last (log of the chunk decay)
+      const float Ln = Lrun + gl;                         // log(e^{G_last} f_c)
+      const bool renorm = Ln < kLogFactorFloor || ch == NC - 1;
+      const float Lnext = renorm ? 0.f : Ln;
+      if (lt < C) {
+        const float eg = __expf(r.g + Lrun);
+        s.BT[lt] = r.b;
+        s.BEG[lt] = r.b * eg;
+        s.EGS[lt] = oscale * eg;
+        s.EL[lt] = __expf(gl - r.g - Lnext);
+        if (lt == 0) {
+          s.DL[0] = __expf(Ln);
+          s.DL[1] = renorm ? 1.f : 0.f;
+        }
+      }
+      Lrun = Lnext;
+    };
+
+    // Interval j (the compute waves work on chunk j from stage j & 1): chunk j+3's loads go into
+    // the register set that held chunk j, chunk j+1 (loaded two intervals earlier) into stage
+    // (j+1) & 1.  Chunk m lives in register set m % 3; past the end the loads repeat the last
+    // chunk.  Every interval is straight-line code, so the compiler's wait counts stay exact and
+    // two chunks stay in flight.
+    const int last = NC - 1;
+    Regs r0, r1, r2;
+    auto interval = [&](Regs& ld, Regs& nx, int j) {
+      const int nl = min(j + 3, last);
+      Stage& sn = st[(j + 1) & 1];
+      load_kq(ld, nl);
+      store_k(sn, nx);
+      lds_barrier();                                     // B1
+      load_tp(ld, nl);
+      store_tp(sn, nx);
+      lds_barrier();                                     // B2
+      load_vg(ld, nl);
+      store_vg(sn, nx, j + 1);
+      store_q(sn, nx);
+      lds_barrier();                                     // B3
+    };
+    auto final_interval = [&]() {                        // writes no chunk
+      lds_barrier();
+      lds_barrier();
+      lds_barrier();
+    };
+    load_kq(r0, 0);
+    load_tp(r0, 0);
+    load_vg(r0, 0);
+    load_kq(r1, min(1, last));
+    load_tp(r1, min(1, last));
+    load_vg(r1, min(1, last));
+    load_kq(r2, min(2, last));
+    load_tp(r2, min(2, last));
+    load_vg(r2, min(2, last));
+    store_k(st[0], r0);
+    store_q(st[0], r0);
+    store_tp(st[0], r0);
+    store_vg(st[0], r0, 0);
+    lds_barrier();                                       // start: stage 0 and SB ready
+    if (NC > 1) {
+      interval(r0, r1, 0);
+      int j = 1;
+      for (; j + 3 < NC; j += 3) {                       // intervals j..j+2 write chunks j+1..j+3
+        interval(r1, r2, j);
+        interval(r2, r0, j + 1);
+        interval(r0, r1, j + 2);
+      }
+      // 1 <= NC - j <= 3 intervals remain, the last of which writes no chunk
+      if (j + 1 < NC) interval(r1, r2, j);
+      if (j + 2 < NC) interval(r2, r0, j + 1);
+    }
+    final_interval();
+  } else {
+    // =========================== compute waves ===========================
+    const int cw = __builtin_amdgcn_readfirstlane(w);   // wave-uniform
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.o + (size_t)bh * Tlen * DV, Tlen * DV * 4);
+    const int tok0 = 16 * cw;                            // this wave's token block
+    // per-lane LDS element offsets
+    const int kq_rd = (tok0 + c) * KP + 4 * (g ^ ((c >> 2) & 3));          // k / q rows
+    const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g) + 32 * cw; // k^T, rows 32cw..
+    const int tp_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // T / P rows
+    const int v_rd = (tok0 + 4 * g + (c >> 2)) * VP + 4 * (c & 3);         // v, transposed read
+    const int frag = lane * 8;                                             // lane's exchange slot
+    const int xhalf = 4 * (cw & 1), xblk = cw >> 1;                        // this wave's RX/VX slot
+
+    floatx4 S[2][NT];                                    // rows 32cw + 16r + 4g + i, column c
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          S[r][nt][ii] = a.h0 ? a.h0[((size_t)bh * DK + 32 * cw + 16 * r + 4 * g + ii) * DV + col0 + 16 * nt + c] : 0.f;
+    auto publish = [&]() {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        *reinterpret_cast<bf16x8*>(SB + (cw * NT + nt) * FRAG + frag) = pack8(S[0][nt], S[1][nt]);
+    };
+    publish();
+    lds_barrier();                                       // start
+
+    for (int ch = 0; ch < NC; ++ch) {
+      const Stage& s = st[ch & 1];
+      // ---- phase A: Y = k S~ and (q S~)^T for this wave's 16 tokens, r -> RX ----
+      floatx4 Y[NT], QT[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) { Y[nt] = zero4(); QT[nt] = zero4(); }
+#pragma unroll
+      for (int kb = 0; kb < DK / 32; ++kb) {
+        const bf16* kp = s.ks + kq_rd + 32 * kb;
+        const bf16* qp = s.qs + kq_rd + 32 * kb;
+        const bf16x8 ka = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
+        const bf16x8 qa = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const bf16x8 sb = *reinterpret_cast<const bf16x8*>(SB + (kb * NT + nt) * FRAG + frag);
+          Y[nt] = mfma_bf16(ka, sb, Y[nt]);               // (k S~)[t][n]
+          QT[nt] = mfma_bf16(sb, qa, QT[nt]);             // (q S~)^T[n][t]
+        }
+      }
+      {
+        const floatx4 bt = *reinterpret_cast<const floatx4*>(s.BT + tok0 + 4 * g);
+        const floatx4 beg = *reinterpret_cast<const floatx4*>(s.BEG + tok0 + 4 * g);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const bf16x4 v4 = lds_read_tr(s.vs + v_rd + 16 * nt);
+          bf16x4 rb;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) rb[ii] = (bf16)fmaf(-beg[ii], Y[nt][ii], bt[ii] * (float)v4[ii]);
+          *reinterpret_cast<bf16x4*>(RX + (xblk * NT + nt) * FRAG + frag + xhalf) = rb;
+        }
+      }
+      lds_barrier();                                     // B1
+      // ---- phase B: v_new = T r for this wave's tokens -> VX, VXs ----
+      floatx4 VN[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) VN[nt] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        if (kb == 0 || cw >= 2) {
+          const bf16* tp = s.ts + tp_rd + 32 * kb;
+          const bf16x8 ta = cat8(*reinterpret_cast<const bf16x4*>(tp), *reinterpret_cast<const bf16x4*>(tp + 16));
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            VN[nt] = mfma_bf16(ta, *reinterpret_cast<const bf16x8*>(RX + (kb * NT + nt) * FRAG + frag), VN[nt]);
+        }
+      }
+      {
+        const floatx4 el = *reinterpret_cast<const floatx4*>(s.EL + tok0 + 4 * g);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          bf16x4 vb, vs;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            vb[ii] = (bf16)VN[nt][ii];
+            vs[ii] = (bf16)(VN[nt][ii] * el[ii]);
+          }
+          *reinterpret_cast<bf16x4*>(VX + (xblk * NT + nt) * FRAG + frag + xhalf) = vb;
+          *reinterpret_cast<bf16x4*>(VXs + (xblk * NT + nt) * FRAG + frag + xhalf) = vs;
+        }
+      }
+      lds_barrier();                                     // B2
+      // ---- phase C: o^T = v_new^T P^T + scale e^G f (q S~)^T -> HBM; S~ update -> SB ----
+      {
+        floatx4 OT[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) OT[nt] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          if (kb == 0 || cw >= 2) {
+            const bf16* pp = s.ps + tp_rd + 32 * kb;
+            const bf16x8 pb = cat8(*reinterpret_cast<const bf16x4*>(pp), *reinterpret_cast<const bf16x4*>(pp + 16));
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+              OT[nt] = mfma_bf16(*reinterpret_cast<const bf16x8*>(VX + (kb * NT + nt) * FRAG + frag), pb, OT[nt]);
+          }
+        }
+        // lane (c, g) holds o[token tok0 + c][columns 16 nt + 4g .. +3]: one 16-byte store each
+        const float egs = s.EGS[tok0 + c];
+        const uint32_t ooff = (uint32_t)(((size_t)ch * C + tok0 + c) * DV + col0 + 4 * g) * 4;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          floatx4 val;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) val[ii] = fmaf(egs, QT[nt][ii], OT[nt][ii]);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, ooff + 64 * nt, 0, 0);
+        }
+      }
+      if (s.DL[1] != 0.f) {
+        const float m = s.DL[0];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) S[r][nt] *= m;
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const bf16* k0 = s.ks + kt_rd + 16 * r;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const bf16x8 at = cat8(lds_read_tr(k0 + 32 * kb * KP), lds_read_tr(k0 + (32 * kb + 16) * KP));
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            S[r][nt] = mfma_bf16(at, *reinterpret_cast<const bf16x8*>(VXs + (kb * NT + nt) * FRAG + frag), S[r][nt]);
+        }
+      }
+      publish();
+      lds_barrier();                                     // B3
+    }
+    if (a.h_final) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii)
+            a.h_final[((size_t)bh * DK + 32 * cw + 16 * r + 4 * g + ii) * DV + col0 + 16 * nt + c] = S[r][nt][ii];
+    }
+  }
+}
+
+}  // namespace pf
