@@ -32,6 +32,7 @@ extern "C" {
 #define PF_ERR_ARG (-1)       /* shape, dtype or null-pointer contract violated */
 #define PF_ERR_WORKSPACE (-2) /* workspace handle missing or too small for this call */
 #define PF_ERR_ALLOC (-3)     /* setup could not allocate its workspace */
+#define PF_ERR_SCRATCH (-4)   /* input larger than the static scratch of pf_gdn_exec_static */
 
 /* Human-readable text for a status code (static storage). */
 const char* pf_status_string(int status);
@@ -62,6 +63,19 @@ int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, 
                 const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
                 int DV, int dtype, float scale, void* ws, void* stream);
 void pf_gdn_teardown(void* ws);
+
+/* The same forward with no workspace argument and no allocation of any kind: no counterpart in
+ * the reference.  It is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  Its workspace is a
+ * file-scope device array of 68 MiB (bf16: up to 4 285 chunks of 64 tokens, the B4 H16 T4096
+ * headline included; fp32: up to 2 159); a larger input returns PF_ERR_SCRATCH and launches
+ * nothing.  The array's device address is looked up once per device on the first call there
+ * (make that call outside any graph capture).  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, or threads) race; serialise them.  Same
+ * arguments as pf_gdn_exec otherwise. */
+int pf_gdn_exec_static(const void* q, const void* k, const void* v, const float* beta,
+                       const float* g, const float* h0, float* o, float* h_final, int B, int H,
+                       int T, int C, int DK, int DV, int dtype, float scale, void* stream);
 
 /* The two stages pf_gdn_exec enqueues, exposed so a caller can time or overlap them
  * separately.  Stage 1 (chunk-local, one workgroup per chunk) writes the within-chunk gate

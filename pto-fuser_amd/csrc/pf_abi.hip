@@ -4,6 +4,7 @@
 // on the caller's stream, and no exec allocates or synchronises.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <new>
 
 #include "../../include/pto_fuser_hip.h"
@@ -56,10 +57,9 @@ bool gdn_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
 
 template <typename E>
 void chunk_local_launch(const void* q, const void* k, const float* beta, const float* g,
-                       float scale, const GdnWorkspace* ws, size_t M, hipStream_t stream) {
+                       float scale, char* base, size_t M, hipStream_t stream) {
   constexpr int C = 64, DK = 128;
   const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
-  char* base = static_cast<char*>(ws->base);
   pf::ChunkLocalArgs a{};
   a.k = k;
   a.q = q;
@@ -94,11 +94,10 @@ int device_cu_count() {
 template <typename E>
 void scan_output_launch(const void* q, const void* k, const void* v, const float* beta,
                        const float* h0, float* o, float* h_final, int BH, int NC,
-                       const GdnWorkspace* ws, hipStream_t stream) {
+                       char* base, hipStream_t stream) {
   constexpr int C = 64, DK = 128, DV = 128, NWC = 2;
   const size_t M = (size_t)BH * NC;
   const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
-  char* base = static_cast<char*>(ws->base);
   pf::ScanOutArgs a{};
   a.q = q;
   a.k = k;
@@ -131,6 +130,22 @@ void scan_output_launch(const void* q, const void* k, const void* v, const float
   }
 }
 
+// Both stages of the forward on the workspace at `base` (the layout of GdnLayout).
+int gdn_forward_on(char* base, const void* q, const void* k, const void* v, const float* beta,
+                   const float* g, const float* h0, float* o, float* h_final, int B, int H, int T,
+                   int C, int dtype, float scale, hipStream_t s) {
+  const size_t M = (size_t)B * H * (T / C);
+  pf::LaunchScope scope;
+  if (dtype == PF_DTYPE_BF16) {
+    chunk_local_launch<bf16>(q, k, beta, g, scale, base, M, s);
+    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, base, s);
+  } else {
+    chunk_local_launch<float>(q, k, beta, g, scale, base, M, s);
+    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, base, s);
+  }
+  return scope.status();
+}
+
 // Shared host checks of the three GDN entry points.
 int gdn_check(int B, int H, int T, int C, int DK, int DV, int dtype, const void* ws) {
   if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
@@ -138,6 +153,40 @@ int gdn_check(int B, int H, int T, int C, int DK, int DV, int dtype, const void*
   if (!w || !w->base || w->bytes < GdnLayout((size_t)B * H * (T / C), C, dtype).total)
     return PF_ERR_WORKSPACE;
   return PF_OK;
+}
+
+// ---- the allocation-free forward ---------------------------------------------------------
+// Its workspace is this file-scope array, 68 MiB: the bf16 headline shape (B4 H16 T4096, 4096
+// chunks: T, P 32 MiB each, G 1 MiB) fits with room to spare; bf16 up to 4 285 chunks of 64
+// tokens, fp32 up to 2 159.  Every GPU the library runs on holds one copy until the process ends.
+constexpr size_t kStaticScratchBytes = size_t(68) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+// Device address of `scratch` on the current device, resolved once per device with
+// hipGetSymbolAddress (in host code the array's name is only a host-side stand-in, never a
+// device address).  Returns nullptr with *status set when the lookup fails.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+void* scratch_on_current_device(int* status) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *status = e != hipSuccess ? static_cast<int>(e) : PF_ERR_ARG;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      *status = e != hipSuccess ? static_cast<int>(e) : PF_ERR_ARG;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -150,6 +199,7 @@ const char* pf_status_string(int status) {
     case PF_ERR_ARG: return "invalid argument (shape, dtype or pointer contract)";
     case PF_ERR_WORKSPACE: return "workspace missing or too small for this call";
     case PF_ERR_ALLOC: return "workspace allocation failed";
+    case PF_ERR_SCRATCH: return "input needs more than the static scratch of pf_gdn_exec_static";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
@@ -199,9 +249,9 @@ int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   pf::LaunchScope scope;
   if (dtype == PF_DTYPE_BF16)
-    chunk_local_launch<bf16>(q, k, beta, g, scale, w, M, s);
+    chunk_local_launch<bf16>(q, k, beta, g, scale, static_cast<char*>(w->base), M, s);
   else
-    chunk_local_launch<float>(q, k, beta, g, scale, w, M, s);
+    chunk_local_launch<float>(q, k, beta, g, scale, static_cast<char*>(w->base), M, s);
   return scope.status();
 }
 
@@ -215,24 +265,37 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
   hipStream_t s = static_cast<hipStream_t>(stream);
   pf::LaunchScope scope;
   if (dtype == PF_DTYPE_BF16)
-    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
+    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C,
+                             static_cast<char*>(w->base), s);
   else
-    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, w, s);
+    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C,
+                              static_cast<char*>(w->base), s);
   return scope.status();
 }
 
 int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
                 const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
                 int DV, int dtype, float scale, void* ws, void* stream) {
-  if (!q || !k || !v || !beta || !o) {
-    const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
-    return st != PF_OK ? st : PF_ERR_ARG;
-  }
-  const int st = pf_gdn_chunk_local_exec(q, k, beta, g, B, H, T, C, DK, DV, dtype, scale, ws,
-                                         stream);
+  const int st = gdn_check(B, H, T, C, DK, DV, dtype, ws);
   if (st != PF_OK) return st;
-  return pf_gdn_scan_output_exec(q, k, v, beta, h0, o, h_final, B, H, T, C, DK, DV, dtype, ws,
-                                 stream);
+  if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
+  return gdn_forward_on(static_cast<char*>(static_cast<GdnWorkspace*>(ws)->base), q, k, v, beta,
+                        g, h0, o, h_final, B, H, T, C, dtype, scale,
+                        static_cast<hipStream_t>(stream));
+}
+
+int pf_gdn_exec_static(const void* q, const void* k, const void* v, const float* beta,
+                       const float* g, const float* h0, float* o, float* h_final, int B, int H,
+                       int T, int C, int DK, int DV, int dtype, float scale, void* stream) {
+  if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
+  if (GdnLayout((size_t)B * H * (T / C), C, dtype).total > kStaticScratchBytes)
+    return PF_ERR_SCRATCH;
+  if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
+  int st = PF_OK;
+  void* base = scratch_on_current_device(&st);
+  if (!base) return st;
+  return gdn_forward_on(static_cast<char*>(base), q, k, v, beta, g, h0, o, h_final, B, H, T, C,
+                        dtype, scale, static_cast<hipStream_t>(stream));
 }
 
 int pf_kkt_inv_exec(const void* k, const float* g, const float* beta, float* A_out, float* T_out,

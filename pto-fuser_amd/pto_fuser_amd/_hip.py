@@ -20,6 +20,7 @@ PF_OK = 0
 PF_ERR_ARG = -1
 PF_ERR_WORKSPACE = -2
 PF_ERR_ALLOC = -3
+PF_ERR_SCRATCH = -4
 
 c_void_p, c_int, c_float, c_size_t = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 
@@ -32,6 +33,7 @@ SIGNATURES = {
     "pf_gdn_setup": (c_void_p, [c_int] * 7),
     "pf_gdn_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
     "pf_gdn_teardown": (None, [c_void_p]),
+    "pf_gdn_exec_static": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p]),
     "pf_gdn_chunk_local_exec": (c_int, [c_void_p] * 4 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
     "pf_gdn_scan_output_exec": (c_int, [c_void_p] * 7 + [c_int] * 7 + [c_void_p, c_void_p]),
     "pf_kkt_inv_exec": (c_int, [c_void_p] * 5 + [c_int] * 5 + [c_void_p]),

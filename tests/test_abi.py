@@ -121,6 +121,20 @@ def test_exec_rejects_contract_violations_before_launch(lib):
                             None) == _hip.PF_ERR_ARG                   # B = 0
 
 
+def test_static_forward_rejects_on_host(lib):
+    """The allocation-free forward refuses an input beyond its static scratch (8192 bf16 chunks)
+    and unsupported shapes before touching the device (safe without one)."""
+    st = lib.pf_gdn_exec_static(1, 1, 1, 1, 1, None, 1, None, 8, 16, 4096, 64, 128, 128,
+                                _hip.PF_DTYPE_BF16, 0.1, None)
+    assert st == _hip.PF_ERR_SCRATCH and "static scratch" in _hip.status_text(st)
+    st = lib.pf_gdn_exec_static(1, 1, 1, 1, 1, None, 1, None, 1, 1, 100, 64, 128, 128,
+                                _hip.PF_DTYPE_BF16, 0.1, None)
+    assert st == _hip.PF_ERR_ARG                                         # T % C != 0
+    st = lib.pf_gdn_exec_static(None, 1, 1, 1, 1, None, 1, None, 1, 1, 128, 64, 128, 128,
+                                _hip.PF_DTYPE_BF16, 0.1, None)
+    assert st == _hip.PF_ERR_ARG                                         # q missing
+
+
 def test_ops_validate_on_host():
     torch = pytest.importorskip("torch")
     from pto_fuser_amd import gdn_chunk_forward, kkt_inverse, tri_inv
