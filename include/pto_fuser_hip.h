@@ -59,6 +59,14 @@ const char* pf_source_hash(void);
  * ------------------------------------------------------------------------------------------ */
 size_t pf_gdn_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
 void* pf_gdn_setup(int B, int H, int T, int C, int DK, int DV, int dtype);
+/* The same workspace in two steps, for a registry whose setup takes no arguments (the
+ * reference's FusedKernel calls setup_sym() bare, fused.py:102-107): pf_gdn_create returns an
+ * empty handle (allocates nothing); pf_gdn_reserve grows it to the shape's size (PF_OK, PF_ERR_ARG
+ * for an unsupported shape, PF_ERR_ALLOC).  A reserve that does not grow allocates nothing and is
+ * safe under HIP graph capture; one that grows waits for the device and must run outside it.
+ * pf_gdn_setup(shape) == pf_gdn_create() + pf_gdn_reserve(shape); pf_gdn_teardown frees either. */
+void* pf_gdn_create(void);
+int pf_gdn_reserve(void* ws, int B, int H, int T, int C, int DK, int DV, int dtype);
 int pf_gdn_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
                 const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
                 int DV, int dtype, float scale, void* ws, void* stream);
@@ -108,6 +116,9 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
  * ------------------------------------------------------------------------------------------ */
 size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
 void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype);
+/* Two-step form of pf_kda_setup, as pf_gdn_create / pf_gdn_reserve above. */
+void* pf_kda_create(void);
+int pf_kda_reserve(void* ws, int B, int H, int T, int C, int DK, int DV, int dtype);
 int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
                 const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,
                 int DV, int dtype, float scale, void* ws, void* stream);

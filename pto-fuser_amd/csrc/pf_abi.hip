@@ -10,6 +10,7 @@
 #include "../../include/pto_fuser_hip.h"
 #include "pf_chunk_local.h"
 #include "pf_status.h"
+#include "pf_workspace.h"
 #include "pf_scan_output.h"
 #include "pf_scan_split.h"
 
@@ -25,10 +26,7 @@ namespace {
 
 using pf::bf16;
 
-struct GdnWorkspace {
-  void* base = nullptr;
-  size_t bytes = 0;
-};
+using GdnWorkspace = pf::Workspace;
 
 constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -218,25 +216,25 @@ size_t pf_gdn_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dt
   return GdnLayout((size_t)B * H * (T / C), C, dtype).total;
 }
 
-void* pf_gdn_setup(int B, int H, int T, int C, int DK, int DV, int dtype) {
+void* pf_gdn_create(void) { return pf::workspace_create(); }
+
+int pf_gdn_reserve(void* ws, int B, int H, int T, int C, int DK, int DV, int dtype) {
   const size_t bytes = pf_gdn_workspace_bytes(B, H, T, C, DK, DV, dtype);
-  if (bytes == 0) return nullptr;
-  GdnWorkspace* ws = new (std::nothrow) GdnWorkspace();
-  if (!ws) return nullptr;
-  if (hipMalloc(&ws->base, bytes) != hipSuccess) {
-    delete ws;
+  if (bytes == 0) return PF_ERR_ARG;
+  return pf::workspace_reserve(static_cast<GdnWorkspace*>(ws), bytes);
+}
+
+void* pf_gdn_setup(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  if (pf_gdn_workspace_bytes(B, H, T, C, DK, DV, dtype) == 0) return nullptr;
+  GdnWorkspace* ws = pf::workspace_create();
+  if (ws && pf_gdn_reserve(ws, B, H, T, C, DK, DV, dtype) != PF_OK) {
+    pf::workspace_destroy(ws);
     return nullptr;
   }
-  ws->bytes = bytes;
   return ws;
 }
 
-void pf_gdn_teardown(void* ws) {
-  GdnWorkspace* w = static_cast<GdnWorkspace*>(ws);
-  if (!w) return;
-  if (w->base) (void)hipFree(w->base);
-  delete w;
-}
+void pf_gdn_teardown(void* ws) { pf::workspace_destroy(static_cast<GdnWorkspace*>(ws)); }
 
 int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, const float* g,
                             int B, int H, int T, int C, int DK, int DV, int dtype, float scale,

@@ -6,6 +6,7 @@
 #include "../../include/pto_fuser_hip.h"
 #include "pf_kda.h"
 #include "pf_status.h"
+#include "pf_workspace.h"
 
 namespace {
 
@@ -13,10 +14,7 @@ using pf::bf16;
 
 constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-struct KdaWorkspace {
-  void* base = nullptr;
-  size_t bytes = 0;
-};
+using KdaWorkspace = pf::Workspace;
 
 // Byte layout of the KDA workspace, M = B*H*T/C chunks:
 //   [ W | U | QE | KR  (each M*C*128 bf16) | P (M*C*C bf16) | DEC (M*128 fp32) ]
@@ -50,25 +48,25 @@ size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dt
   return KdaLayout((size_t)B * H * (T / C), C, DK).total;
 }
 
-void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype) {
+void* pf_kda_create(void) { return pf::workspace_create(); }
+
+int pf_kda_reserve(void* ws, int B, int H, int T, int C, int DK, int DV, int dtype) {
   const size_t bytes = pf_kda_workspace_bytes(B, H, T, C, DK, DV, dtype);
-  if (bytes == 0) return nullptr;
-  KdaWorkspace* ws = new (std::nothrow) KdaWorkspace();
-  if (!ws) return nullptr;
-  if (hipMalloc(&ws->base, bytes) != hipSuccess) {
-    delete ws;
+  if (bytes == 0) return PF_ERR_ARG;
+  return pf::workspace_reserve(static_cast<KdaWorkspace*>(ws), bytes);
+}
+
+void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype) {
+  if (pf_kda_workspace_bytes(B, H, T, C, DK, DV, dtype) == 0) return nullptr;
+  KdaWorkspace* ws = pf::workspace_create();
+  if (ws && pf_kda_reserve(ws, B, H, T, C, DK, DV, dtype) != PF_OK) {
+    pf::workspace_destroy(ws);
     return nullptr;
   }
-  ws->bytes = bytes;
   return ws;
 }
 
-void pf_kda_teardown(void* ws) {
-  KdaWorkspace* w = static_cast<KdaWorkspace*>(ws);
-  if (!w) return;
-  if (w->base) (void)hipFree(w->base);
-  delete w;
-}
+void pf_kda_teardown(void* ws) { pf::workspace_destroy(static_cast<KdaWorkspace*>(ws)); }
 
 int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, const float* g,
                 const float* h0, float* o, float* h_final, int B, int H, int T, int C, int DK,

@@ -8,7 +8,8 @@ policy, transforms, templates and ``compile_program``.
 from . import _hip
 from .compile import CompileResult, compile_program
 from .cost import CostModel, Features, Prediction
-from .executor import StagedExecutor, library_modes
+from .dataflow import Dataflow, ProgramEdit
+from .executor import StagedExecutor
 from .fused import (FusedContract, FusedKernel, FusedKernelRegistry, default_fused_registry,
                     shared_fused_registry)
 from .fusion import FusionDecision, decide, format_decisions as format_fusion_decisions
@@ -16,20 +17,22 @@ from .gate import GateResult, frob_rel, gate_determinism, gate_frob_rel, gate_ou
 from .graph import CaptureExecutor, GraphReplayExecutor
 from .ir import (EinsumNode, FusedNode, Node, OpaqueNode, Program, TensorOp, TensorRef,
                  VecGlueNode)
-from .ops import chunk_scan, gated_qk, gdn_chunk_forward, kda_chunk_forward, kkt_inverse, qkv_flash, tri_inv
+from .ops import (chunk_scan, gated_qk, gdn_chunk_forward, kda_chunk_forward, kkt_inverse,
+                  qkv_flash, tri_inv)
 from .policy import PlannedTransform, Policy
 from .registry import OpaqueContract, OpaqueRegistry, capture_mode, default_registry
 from .report import CompilationReport, TransformRecord
 from .template import (EpilogueUnit, FuseChunkOFlash, FuseContractionEpilogue,
-                       FusePerDimChunkOFlash, Template, default_templates, epilogue_report,
-                       extract_epilogue_unit)
+                       FusePerDimChunkOFlash, ScoreTemplate, Template, default_templates,
+                       epilogue_report, extract_epilogue_unit)
 from .transform import (EnableDirectReads, EnableFusedStore, Transform, TransformResult,
                         canonicalize)
 
 __all__ = [
-    "gdn_chunk_forward", "kda_chunk_forward", "kkt_inverse", "tri_inv", "gated_qk", "qkv_flash", "chunk_scan",
+    "gdn_chunk_forward", "kda_chunk_forward", "kkt_inverse", "tri_inv", "gated_qk", "qkv_flash",
+    "chunk_scan",
     "TensorRef", "Node", "EinsumNode", "OpaqueNode", "VecGlueNode", "TensorOp", "FusedNode",
-    "Program", "StagedExecutor", "library_modes", "OpaqueRegistry", "OpaqueContract",
+    "Program", "Dataflow", "ProgramEdit", "StagedExecutor", "OpaqueRegistry", "OpaqueContract",
     "default_registry", "capture_mode", "GateResult", "FusedContract", "FusedKernel",
     "FusedKernelRegistry", "default_fused_registry", "shared_fused_registry", "frob_rel",
     "gate_frob_rel", "gate_outputs", "gate_determinism", "CaptureExecutor",
@@ -37,6 +40,6 @@ __all__ = [
     "TransformResult", "canonicalize", "EnableDirectReads", "EnableFusedStore", "CostModel",
     "Features", "Prediction", "Policy", "PlannedTransform", "CompilationReport",
     "TransformRecord", "CompileResult", "compile_program", "EpilogueUnit",
-    "extract_epilogue_unit", "Template", "default_templates", "FuseContractionEpilogue",
+    "extract_epilogue_unit", "ScoreTemplate", "Template", "default_templates", "FuseContractionEpilogue",
     "FuseChunkOFlash", "FusePerDimChunkOFlash", "epilogue_report",
 ]

@@ -31,6 +31,8 @@ SIGNATURES = {
     "pf_source_hash": (ctypes.c_char_p, []),
     "pf_gdn_workspace_bytes": (c_size_t, [c_int] * 7),
     "pf_gdn_setup": (c_void_p, [c_int] * 7),
+    "pf_gdn_create": (c_void_p, []),
+    "pf_gdn_reserve": (c_int, [c_void_p] + [c_int] * 7),
     "pf_gdn_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
     "pf_gdn_teardown": (None, [c_void_p]),
     "pf_gdn_exec_static": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p]),
@@ -43,6 +45,8 @@ SIGNATURES = {
     "pf_scan_exec": (c_int, [c_void_p] * 7 + [c_int] * 8 + [c_void_p]),
     "pf_kda_workspace_bytes": (c_size_t, [c_int] * 7),
     "pf_kda_setup": (c_void_p, [c_int] * 7),
+    "pf_kda_create": (c_void_p, []),
+    "pf_kda_reserve": (c_int, [c_void_p] + [c_int] * 7),
     "pf_kda_exec": (c_int, [c_void_p] * 8 + [c_int] * 7 + [c_float, c_void_p, c_void_p]),
     "pf_kda_teardown": (None, [c_void_p]),
     "pf_gated_qk_setup": (c_void_p, []),

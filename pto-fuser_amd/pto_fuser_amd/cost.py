@@ -111,10 +111,6 @@ class CostModel:
             saved = _us(max(staged - fused, 0), 10 * nc + 20)
             return Prediction(saved, f"whole forward in 2 kernels: {(staged - fused) / 1e6:.1f} MB "
                                      f"of stage traffic and ~{10 * nc + 20} launches removed")
-        if transform_name == "batch-chunk-intra-score":
-            saved = _us(2 * M * C * C * 4, 2 * (nc - 1))
-            return Prediction(saved, f"{nc} per-chunk intra scores -> one launch over {M} chunks",
-                              v2=v2)
         if transform_name in ("fuse-chunk-o-flash", "fuse-perdim-chunk-o-flash"):
             # the [M,C,C] score is written in fp32, cast, masked/gated and re-read by the
             # second contraction in the staged form; the flash kernel keeps it in LDS.

@@ -1,10 +1,18 @@
-"""Fused-kernel registry: the FusedNode backend (src/pto_fuser/fused.py:1-598).
+"""Fused-kernel registry: the FusedNode backend.
 
 A ``FusedNode`` names one HIP kernel of libptofuser_hip.so that stands in for a staged
-sub-chain.  The registry maps the key to a recipe: the C entry point, the shape key, the launch
-adapter (operand layout/dtype, output allocation) and the pinned contract.  Launches go on the
-current torch stream with no host synchronisation and no allocation inside the library, so a
-fused node is capturable into a HIP graph.
+sub-chain.  The registry maps the key to a recipe and builds, per shape key, a ``FusedKernel``:
+the loaded library, the workspace its setup symbol returns, and the launch adapter (operand
+layout and dtype, output allocation).  Launches go on the current torch stream with no host
+synchronisation and no allocation inside the library, so a fused node is capturable into a HIP
+graph.
+
+Recipes have the fields of the reference's recipe (src/pto_fuser/fused.py:119-127: src_dir,
+src_file, defines, setup_sym, teardown_sym, bind, launch(lib, ws, inputs, params), contract), so
+a recipe written for either registry loads in both.  Loading differs: the reference compiles
+``src_file`` with bisheng into one ``.so`` per ``-D`` set (fused.py:58-77); this registry loads a
+prebuilt ``.so`` as it lies (this build's library is compiled once and dispatches shapes at run
+time), and a recipe with an empty ``src_file`` launches without a library.
 
 Keys and contracts are the reference's, so its programs and transforms name the same kernels:
 
@@ -19,16 +27,11 @@ Keys and contracts are the reference's, so its programs and transforms name the 
   kda_forward                       pf_kda_exec        the whole KDA forward (two kernels)
 
 The last two have no counterpart among the reference's keys: they are the fused forwards of
-this build (``ops.gdn_chunk_forward`` / ``ops.kda_chunk_forward``) offered to the compile stack,
-so a program the policy is allowed to collapse runs as the two fused kernels instead of its
-staged contractions.  Their workspaces are the ops module's cached ones (allocated on the first,
-eager call; a captured graph reuses them).
+this build (``ops.gdn_chunk_forward`` / ``ops.kda_chunk_forward``) offered to the compile stack.
+Their workspaces are the ops module's cached per-stream ones.
 
 Differences from the reference, all deliberate:
 
-* No per-shape compilation.  The reference builds one ``.so`` per ``-D`` set with bisheng; here
-  every shape dispatches at run time onto instantiations inside the one library, so ``defines``
-  only keys the kernel cache.
 * The ``_v2`` keys (the reference's FFTS-interleave / L2-ring variants, which exist to stop its
   intermediate scores round-tripping HBM) run the same kernels as the plain keys: the HIP kernels
   never write the score to HBM in the first place.
@@ -39,20 +42,19 @@ Differences from the reference, all deliberate:
 """
 from __future__ import annotations
 
+import ctypes
+import os
 from dataclasses import dataclass
 from typing import Any, Callable, Dict, List, Optional, Tuple
 
 import torch
 
-from . import ops
+from . import _build, _hip, ops
 
 __all__ = ["FusedContract", "FusedKernel", "FusedKernelRegistry", "default_fused_registry",
            "shared_fused_registry"]
 
 
-# --------------------------------------------------------------------------- #
-#  contract + runner
-# --------------------------------------------------------------------------- #
 @dataclass
 class FusedContract:
     """The pinned interface of one fused kernel."""
@@ -63,54 +65,82 @@ class FusedContract:
     notes: str = ""
 
 
-class FusedKernel:
-    """One recipe bound to one shape key.  ``run`` adapts the operands and launches on the
-    current stream; there is no per-kernel workspace to set up or tear down (the stage kernels
-    keep their intermediates on chip), so ``close`` has nothing to free."""
-
-    def __init__(self, key: str, launch: Callable, entry: str) -> None:
-        self.key, self._launch, self.entry = key, launch, entry
-
-    def run(self, inputs: List[torch.Tensor], params: dict) -> List[torch.Tensor]:
-        return self._launch(inputs, params)
-
-    def close(self) -> None:
-        pass
-
-
 @dataclass
 class _Recipe:
-    entry: str                                   # C entry point in libptofuser_hip.so
-    defines: Callable[[dict], Dict[str, int]]    # params -> shape key
-    launch: Callable                             # (inputs, params) -> [outputs]
+    src_dir: str
+    src_file: str                                 # prebuilt .so, or "" for a library-free launch
+    defines: Callable[[dict], Dict[str, int]]     # params -> shape key (the kernel cache key)
+    setup_sym: str                                # workspace constructor ("" = none)
+    teardown_sym: str                             # workspace destructor ("" = none)
+    bind: Callable[[Any], None]                   # argtypes / restypes on the loaded library
+    launch: Callable                              # (lib, ws, inputs, params) -> [outputs]
     contract: FusedContract
+
+
+class FusedKernel:
+    """One recipe at one shape key: the library, its workspace and the launch adapter."""
+
+    def __init__(self, lib: Any, launch: Callable, setup_sym: str, teardown_sym: str) -> None:
+        self._lib, self._launch, self._teardown = lib, launch, teardown_sym
+        self._ws = ctypes.c_void_p(getattr(lib, setup_sym)()) if lib is not None and setup_sym \
+            else ctypes.c_void_p(0)
+
+    def run(self, inputs: List[torch.Tensor], params: dict) -> List[torch.Tensor]:
+        return self._launch(self._lib, self._ws, inputs, params)
+
+    def close(self) -> None:
+        if self._ws and self._teardown and self._lib is not None:
+            getattr(self._lib, self._teardown)(self._ws)
+        self._ws = ctypes.c_void_p(0)
 
 
 class FusedKernelRegistry:
     def __init__(self) -> None:
         self._recipes: Dict[str, _Recipe] = {}
         self._cache: Dict[Tuple, FusedKernel] = {}
+        self._libs: Dict[str, Any] = {}
 
     def register(self, key: str, recipe: _Recipe) -> None:
         if key in self._recipes:
-            raise ValueError(f"fused kernel {key!r} already registered")
+            raise ValueError(f"fused kernel {key!r} is already registered")
         self._recipes[key] = recipe
 
     def keys(self) -> List[str]:
-        return list(self._recipes)
+        return sorted(self._recipes)
+
+    def _recipe(self, key: str) -> _Recipe:
+        try:
+            return self._recipes[key]
+        except KeyError:
+            raise KeyError(f"no fused kernel registered under {key!r}") from None
 
     def contract(self, key: str) -> FusedContract:
-        if key not in self._recipes:
-            raise KeyError(f"no fused kernel registered under {key!r}")
-        return self._recipes[key].contract
+        return self._recipe(key).contract
+
+    def recipe(self, key: str) -> _Recipe:
+        return self._recipe(key)
+
+    def _library(self, r: _Recipe):
+        """The loaded library of a recipe, bound once per file (None for a library-free one)."""
+        if not r.src_file:
+            return None
+        path = os.path.join(r.src_dir, r.src_file)
+        if path not in self._libs:
+            if not path.endswith(".so"):
+                raise RuntimeError(f"{path}: this registry loads prebuilt shared libraries only "
+                                   f"(build the kernel library first)")
+            own = os.path.abspath(path) == os.path.abspath(_hip.lib_path())
+            lib = _hip.load() if own else ctypes.CDLL(path)
+            r.bind(lib)
+            self._libs[path] = lib
+        return self._libs[path]
 
     def kernel(self, key: str, params: dict) -> FusedKernel:
-        if key not in self._recipes:
-            raise KeyError(f"no fused kernel registered under {key!r}")
-        r = self._recipes[key]
+        r = self._recipe(key)
         ck = (key, tuple(sorted(r.defines(params).items())))
         if ck not in self._cache:
-            self._cache[ck] = FusedKernel(key, r.launch, r.entry)
+            self._cache[ck] = FusedKernel(self._library(r), r.launch, r.setup_sym,
+                                            r.teardown_sym)
         return self._cache[ck]
 
     def run(self, key: str, inputs: List[torch.Tensor], params: dict) -> List[torch.Tensor]:
@@ -314,30 +344,49 @@ def _shape_key(*names):
     return lambda p: {n: p[n] for n in names if n in p}
 
 
+def _bound(lib) -> None:
+    """The in-tree library is bound by its loader (_hip.load binds every entry point)."""
+
+
+def _adapt(fn: Callable) -> Callable:
+    """A launch adapter in the recipe convention: the ops module holds the library and the
+    workspaces, so the adapter needs only the operands."""
+    return lambda lib, ws, inputs, params: fn(inputs, params)
+
+
 _BF, _F32 = torch.bfloat16, torch.float32
+
+
+def _hip_recipe(entry: str, defines, launch: Callable, contract: FusedContract) -> _Recipe:
+    """A recipe on libptofuser_hip.so; ``entry`` names the exec symbol whose setup / teardown
+    pair the recipe holds (the stage kernels export NULL-returning ones)."""
+    stem = {"pf_scan_exec": "pf_scan", "pf_gated_qk_exec": "pf_gated_qk",
+            "pf_qkv_flash_exec": "pf_qkv_flash"}.get(entry, "")
+    return _Recipe(src_dir=_build.LIB_DIR, src_file=_build.LIB_NAME, defines=defines,
+                   setup_sym=f"{stem}_setup" if stem else "",
+                   teardown_sym=f"{stem}_teardown" if stem else "",
+                   bind=_bound, launch=_adapt(launch), contract=contract)
 
 
 def default_fused_registry() -> FusedKernelRegistry:
     reg = FusedKernelRegistry()
-    reg.register("chunk_h_scan", _Recipe(
-        entry="pf_scan_exec", defines=_shape_key("B", "H", "nc", "perdim_decay"),
-        launch=_scan_launch,
-        contract=FusedContract(
+    reg.register("chunk_h_scan", _hip_recipe(
+        "pf_scan_exec", _shape_key("B", "H", "nc", "perdim_decay"), _scan_launch,
+        FusedContract(
             in_slots=["w", "u", "k", "decay"], in_dtypes=[_BF, _BF, _BF, _F32],
             out_names=["h_out", "final"], out_dtype=_BF,
             notes="resident-state chunk recurrence; w/u/k [B,nc,C,H,D]; decay [B,H,nc] scalar "
                   "or [B,H,nc,D] per key channel (perdim_decay=True); C in {16,32,64,128}, "
                   "D in {64,128}; fp32 operands run fp32 end to end")))
-    reg.register("kkt_gated", _Recipe(
-        entry="pf_gated_qk_exec", defines=_shape_key("nc", "H"), launch=_kkt_launch,
-        contract=FusedContract(
+    reg.register("kkt_gated", _hip_recipe(
+        "pf_gated_qk_exec", _shape_key("nc", "H"), _kkt_launch,
+        FusedContract(
             in_slots=["k", "g_sum", "beta"], in_dtypes=[_BF, _F32, _F32],
             out_names=["L"], out_dtype=_BF,
             notes="gated strict-lower k·kᵀ on the token layout k [1,T,H,D] -> L [T,H,C]")))
-    reg.register("gated_qk", _Recipe(
-        entry="pf_gated_qk_exec", defines=_shape_key("nc", "H", "causal"),
-        launch=_gated_qk_launch,
-        contract=FusedContract(
+    reg.register("gated_qk", _hip_recipe(
+        "pf_gated_qk_exec", _shape_key("nc", "H", "causal"), _gated_qk_launch,
+        FusedContract(
             in_slots=["a", "b", "g_sum", "beta"], in_dtypes=[_BF, _BF, _F32, _F32],
             out_names=["L"], out_dtype=_BF,
             notes="gated a·bᵀ on the token layout a,b [1,T,H,D]; chunk_o score = "
@@ -349,19 +398,17 @@ def default_fused_registry() -> FusedKernelRegistry:
              ["a", "b", "g_native", "beta_native"],
              "native a·bᵀ + gate/mask epilogue; chunk_o Aqk = (q, k, beta=1, causal)")):
         for suffix in ("", "_v2"):
-            reg.register(key + suffix, _Recipe(
-                entry="pf_gated_qk_exec", defines=_shape_key("nc", "H", "C", "D", "causal"),
-                launch=launch,
-                contract=FusedContract(
+            reg.register(key + suffix, _hip_recipe(
+                "pf_gated_qk_exec", _shape_key("nc", "H", "C", "D", "causal"), launch,
+                FusedContract(
                     in_slots=list(slots), in_dtypes=[_BF] * (len(slots) - 2) + [_F32, _F32],
                     out_names=["L"], out_dtype=_BF,
                     notes=note + ("; same kernel as the plain key (the score never leaves the "
                                   "chip in either)" if suffix else ""))))
     for suffix in ("", "_v2"):
-        reg.register("qk_prologue" + suffix, _Recipe(
-            entry="pf_gated_qk_exec", defines=_shape_key("nc", "H", "C", "D"),
-            launch=_prologue_launch,
-            contract=FusedContract(
+        reg.register("qk_prologue" + suffix, _hip_recipe(
+            "pf_gated_qk_exec", _shape_key("nc", "H", "C", "D"), _prologue_launch,
+            FusedContract(
                 in_slots=["q", "k", "P", "invP"], in_dtypes=[_BF, _BF, _F32, _F32],
                 out_names=["L"], out_dtype=_BF,
                 notes="per-channel prologue tril((q⊙P)·(k⊙invP)ᵀ); q/k/P/invP [M,C,D], "
@@ -376,24 +423,20 @@ def default_fused_registry() -> FusedKernelRegistry:
         in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
         notes="per-channel chunk_o flash: o = tril((q⊙coef_ag)·(k⊙coef_bg)ᵀ)·v in one launch")
     for suffix in ("", "_v2"):
-        reg.register("qkv_flash_native" + suffix, _Recipe(
-            entry="pf_qkv_flash_exec", defines=_shape_key("nc", "H", "C", "D", "DV"),
-            launch=_qkv_launch, contract=qkv))
-        reg.register("qkvp_flash_native" + suffix, _Recipe(
-            entry="pf_qkv_flash_exec", defines=_shape_key("nc", "H", "C", "D", "DV"),
-            launch=_qkvp_launch, contract=qkvp))
-    reg.register("gdn_forward", _Recipe(
-        entry="pf_gdn_exec", defines=_shape_key("B", "H", "nc", "C", "D"),
-        launch=_gdn_forward_launch,
-        contract=FusedContract(
+        reg.register("qkv_flash_native" + suffix, _hip_recipe(
+            "pf_qkv_flash_exec", _shape_key("nc", "H", "C", "D", "DV"), _qkv_launch, qkv))
+        reg.register("qkvp_flash_native" + suffix, _hip_recipe(
+            "pf_qkv_flash_exec", _shape_key("nc", "H", "C", "D", "DV"), _qkvp_launch, qkvp))
+    reg.register("gdn_forward", _hip_recipe(
+        "pf_gdn_exec", _shape_key("B", "H", "nc", "C", "D"), _gdn_forward_launch,
+        FusedContract(
             in_slots=["q", "k", "v", "g_native", "beta_native"],
             in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
             notes="whole GDN forward: q/k/v [M,C,D] (bf16, or fp32 end to end), cumulative "
                   "gate g_native and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64, D = 128")))
-    reg.register("kda_forward", _Recipe(
-        entry="pf_kda_exec", defines=_shape_key("B", "H", "nc", "C", "D"),
-        launch=_kda_forward_launch,
-        contract=FusedContract(
+    reg.register("kda_forward", _hip_recipe(
+        "pf_kda_exec", _shape_key("B", "H", "nc", "C", "D"), _kda_forward_launch,
+        FusedContract(
             in_slots=["q", "k", "v", "g_native", "beta_native"],
             in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
             notes="whole KDA forward: q/k/v [M,C,D] bf16, per-channel cumulative gate "

@@ -1,15 +1,16 @@
-"""Graph-replay backend: a whole Program captured into one HIP graph (src/pto_fuser/graph.py).
+"""Graph replay: a whole Program recorded once as a HIP graph and replayed as one launch.
 
-``GraphReplayExecutor.capture`` runs the program eagerly a few times on a side stream (first-call
-library setup — hipBLASLt heuristics, the HIP library load — happens there, outside the graph),
-then records one run into a ``torch.cuda.CUDAGraph`` (a hipGraph on ROCm) over static input
-buffers.  ``replay`` copies new operands into those buffers and launches the graph: the program's
-tens to hundreds of kernel launches become one graph launch.
+The reference records its programs with NPU graphs (src/pto_fuser/graph.py:80-138); here the
+recording is a ``torch.cuda.CUDAGraph``, which is a hipGraph on ROCm.  ``capture``:
 
-Everything the program launches is capturable as it stands: the HIP stage kernels enqueue on the
-current stream and allocate nothing, the opaque tri-inverse needs no host synchronisation (it
-launches on the current stream, unlike the reference's raw launch), and torch's own kernels
-allocate from the graph's private pool.  Shapes are fixed at capture time.
+1. copies the bindings into static input buffers (replays read from them);
+2. runs the program eagerly ``warmup`` times on a private stream — first-call work (the HIP
+   library load, GEMM heuristics, the fused kernels' per-stream workspaces) happens there;
+3. records one run on that same stream, inside ``capture_mode()``.
+
+``replay`` copies new operands of the captured shapes into the static buffers and launches the
+graph.  Every node of a program is capturable as it stands: the HIP kernels enqueue on the
+current stream and allocate nothing, and torch's kernels allocate from the graph's private pool.
 """
 from __future__ import annotations
 
@@ -17,95 +18,63 @@ from typing import Dict, Optional
 
 import torch
 
-from . import registry as _registry
-from .executor import StagedExecutor, _cast, library_modes
+from .executor import StagedExecutor
 from .fused import FusedKernelRegistry
-from .ir import EinsumNode, Program
-from .registry import OpaqueRegistry
+from .ir import Program
+from .registry import OpaqueRegistry, capture_mode
 
 __all__ = ["CaptureExecutor", "GraphReplayExecutor"]
 
 
 class CaptureExecutor(StagedExecutor):
-    """A StagedExecutor whose contractions go through per-node runners built once (with the
-    node's read-mode / fused-store annotations fixed at build time), so the captured region is
-    launches only."""
+    """The staged executor as used for recording: every step runs inside ``capture_mode()``."""
 
-    def __init__(self, registry: Optional[OpaqueRegistry] = None,
-                 fused: Optional[FusedKernelRegistry] = None) -> None:
-        super().__init__(registry, fused=fused)
-        self._runners: Dict[tuple, object] = {}
-
-    def _exec(self, node, env):
-        if isinstance(node, EinsumNode):
-            a, b = (env[n] for n in node.inputs)
-            return _cast(self._runner(node, a, b)(a, b), node.out_dtype)
-        return super()._exec(node, env)
-
-    def _runner(self, node: EinsumNode, a: torch.Tensor, b: torch.Tensor):
-        key = (node.equation, tuple(a.shape), tuple(b.shape), a.dtype, b.dtype,
-               node.read_mode, node.fuse_out)
-        runner = self._runners.get(key)
-        if runner is None:
-            eq, mode, fuse, core = node.equation, node.read_mode, node.fuse_out, self.einsum
-
-            def runner(x, y, eq=eq, mode=mode, fuse=fuse, core=core):
-                with library_modes(mode, fuse):
-                    return core(eq, x, y)
-            self._runners[key] = runner
-        return runner
+    def run(self, program: Program, bindings: Dict[str, torch.Tensor], return_env: bool = False):
+        with capture_mode():
+            return super().run(program, bindings, return_env)
 
 
 class GraphReplayExecutor:
-    """Capture a Program into one HIP graph; replay it as a single launch."""
-
     def __init__(self, registry: Optional[OpaqueRegistry] = None,
                  fused: Optional[FusedKernelRegistry] = None) -> None:
-        self._exec = CaptureExecutor(registry, fused)
+        self._eager = StagedExecutor(registry, fused=fused)
+        self._recorder = CaptureExecutor(registry, fused=fused)
         self._graph: Optional[torch.cuda.CUDAGraph] = None
-        self._static_in: Dict[str, torch.Tensor] = {}
-        self._out: Dict[str, torch.Tensor] = {}
+        self._inputs: Dict[str, torch.Tensor] = {}
+        self._outputs: Dict[str, torch.Tensor] = {}
         self.program: Optional[Program] = None
 
     def capture(self, program: Program, bindings: Dict[str, torch.Tensor],
                 warmup: int = 3) -> "GraphReplayExecutor":
-        missing = [n for n in program.inputs if n not in bindings]
-        if missing:
-            raise ValueError(f"missing bindings for inputs: {missing}")
-        self._static_in = {k: bindings[k].clone() for k in program.inputs}
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
+        absent = [n for n in program.inputs if n not in bindings]
+        if absent:
+            raise ValueError(f"missing bindings for program inputs: {absent}")
+        self._inputs = {n: bindings[n].clone() for n in program.inputs}
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
             for _ in range(max(1, warmup)):
-                self._exec.run(program, self._static_in, return_env=True)
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-
+                self._eager.run(program, self._inputs)
+        stream.synchronize()
         graph = torch.cuda.CUDAGraph()
-        # captured on the warmup stream: the fused kernels' workspaces are cached per stream
-        # and were allocated there by the warmup (capture itself must not allocate them)
-        with torch.cuda.graph(graph, stream=side):
-            with _registry.capture_mode():
-                env = self._exec.run(program, self._static_in, return_env=True)
+        with torch.cuda.graph(graph, stream=stream):
+            env = self._recorder.run(program, self._inputs, return_env=True)
         torch.cuda.synchronize()
-        self._graph = graph
-        self.program = program
-        self._out = {name: env[name] for name in program.outputs}
+        self._graph, self.program = graph, program
+        self._outputs = {n: env[n] for n in program.outputs}
         return self
 
     def replay(self, bindings: Dict[str, torch.Tensor],
                clone: bool = True) -> Dict[str, torch.Tensor]:
-        """Replay on ``bindings`` (the captured shapes).  The outputs live in the graph's pool;
-        ``clone=True`` returns copies that survive the next replay."""
+        """Launch the graph on ``bindings`` (the captured shapes).  The outputs live in the
+        graph's pool and are overwritten by the next replay; ``clone=True`` returns copies."""
         if self._graph is None:
-            raise RuntimeError("capture() must be called before replay()")
-        for name, buf in self._static_in.items():
+            raise RuntimeError("replay() needs a graph: call capture() first")
+        for name, buf in self._inputs.items():
             src = bindings[name]
-            if tuple(src.shape) != tuple(buf.shape):
-                raise ValueError(f"replay shape {tuple(src.shape)} for {name!r} != captured "
-                                 f"{tuple(buf.shape)} (a new shape needs a new capture)")
+            if src.shape != buf.shape:
+                raise ValueError(f"{name!r} has shape {tuple(src.shape)} but the graph was "
+                                 f"captured for {tuple(buf.shape)}; capture again for a new shape")
             buf.copy_(src)
         self._graph.replay()
-        if clone:
-            return {k: v.clone() for k, v in self._out.items()}
-        return dict(self._out)
+        return {n: (t.clone() if clone else t) for n, t in self._outputs.items()}

@@ -1,23 +1,34 @@
-"""Transforms: pure ``Program -> Program`` rewrites (src/pto_fuser/transform.py:1-183).
+"""Program rewrites: the Transform interface, the canonical form, the annotation levers.
 
-A transform matches a structural pattern and rewrites it; it never measures or touches the
-device.  Whether it is worth trying is the cost model's and policy's call, whether the rewrite is
-correct and faster is the compile driver's.  Each carries a kebab-case ``name``, a ``summary``,
-construction options (the forward's dims), ``match`` (number of rewritable sites, 0 = not
-applicable) and ``apply`` (returns a ``TransformResult``).
+Interface (the reference's, src/pto_fuser/transform.py:49-65: a kebab-case ``name``, a
+``summary``, ``match(program) -> sites`` and ``apply(program) -> TransformResult``; a transform
+never touches the device — whether it is worth trying is the cost model's call, whether it is
+right and faster the compile driver's).  Here every transform is written as two hooks over the
+shared dataflow view:
 
-This module holds the IR helpers, the canonical form, and the two universal annotation levers;
-the forward-shaped rewrites live in ``transforms/`` and ``template.py``.
+* ``sites(flow)``  — the non-overlapping places the rewrite applies to (any objects);
+* ``rewrite(flow, site, edit)`` — record the replacement of one site in a ``ProgramEdit`` and
+  return a one-line note.
+
+``match`` counts the sites; ``apply`` rewrites all of them against the original indices in one
+pass.  ``stage`` places a transform in the policy's pipeline (see policy.py).
+
+The two annotation levers flip the ``read_mode`` / ``fuse_out`` fields of every contraction.
+They are annotations only on MI355X: they are what the reference's contraction library
+(pto-einsum) reads to pick operand layouts, and the contraction backend here (the staged
+executor's fp32 GEMMs) chooses its own layouts.  They are kept so that programs, reports and the
+lowered-kernel contract read as the reference's do.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass, replace
-from typing import Dict, List
+from typing import Any, List
 
-from .ir import EinsumNode, Node, Program, node_outputs
+from .dataflow import Dataflow, ProgramEdit
+from .ir import EinsumNode, Program
 
-__all__ = ["TransformResult", "Transform", "producer_index", "consumer_map", "splice",
-           "canonicalize", "EnableDirectReads", "EnableFusedStore"]
+__all__ = ["TransformResult", "Transform", "canonicalize", "AnnotationLever",
+           "EnableDirectReads", "EnableFusedStore"]
 
 
 @dataclass
@@ -31,96 +42,70 @@ class TransformResult:
 class Transform:
     name: str = "transform"
     summary: str = ""
+    stage: str = "structural"          # whole | structural | fusion | epilogue | annotation
+    no_site_note: str = "no site"
 
-    def match(self, program: Program) -> int:      # pragma: no cover - abstract
+    def sites(self, flow: Dataflow) -> List[Any]:          # pragma: no cover - abstract
         raise NotImplementedError
 
-    def apply(self, program: Program) -> TransformResult:   # pragma: no cover - abstract
+    def rewrite(self, flow: Dataflow, site: Any, edit: ProgramEdit) -> str:  # pragma: no cover
         raise NotImplementedError
+
+    def match(self, program: Program) -> int:
+        return len(self.sites(Dataflow(program)))
+
+    def apply(self, program: Program) -> TransformResult:
+        flow = Dataflow(program)
+        found = self.sites(flow)
+        if not found:
+            return TransformResult(program, False, 0, self.no_site_note)
+        edit = ProgramEdit(program)
+        notes = [self.rewrite(flow, site, edit) for site in found]
+        return TransformResult(edit.build(), True, len(found), "; ".join(n for n in notes if n))
 
     def __str__(self) -> str:
         return self.name
 
 
-def producer_index(program: Program) -> Dict[str, int]:
-    """name -> index of the step that binds it (the last one wins)."""
-    out: Dict[str, int] = {}
-    for i, node in enumerate(program.nodes):
-        for name in node_outputs(node):
-            out[name] = i
-    return out
-
-
-def consumer_map(program: Program) -> Dict[str, List[int]]:
-    """name -> indices of the steps that read it."""
-    out: Dict[str, List[int]] = {}
-    for i, node in enumerate(program.nodes):
-        for name in node.inputs:
-            out.setdefault(name, []).append(i)
-    return out
-
-
-def splice(program: Program, drop: set, insert_at: int, new_nodes: List[Node]) -> Program:
-    """Remove the steps at ``drop`` and insert ``new_nodes`` just before the step that was at
-    ``insert_at`` (appended if that index is past the end).  The result is re-validated."""
-    nodes: List[Node] = []
-    placed = False
-    for i, node in enumerate(program.nodes):
-        if i == insert_at:
-            nodes.extend(new_nodes)
-            placed = True
-        if i not in drop:
-            nodes.append(node)
-    if not placed:
-        nodes.extend(new_nodes)
-    return Program(nodes=nodes, inputs=list(program.inputs), outputs=list(program.outputs))
-
-
-def _rebuild(program: Program, nodes: List[Node]) -> Program:
-    return Program(nodes=nodes, inputs=list(program.inputs), outputs=list(program.outputs))
-
-
 def canonicalize(program: Program) -> Program:
-    """The always-valid baseline: every contraction reads contiguous operands (``NN``) and
-    returns a contiguous result (no fused store)."""
-    return _rebuild(program, [replace(n, read_mode="NN", fuse_out=False)
-                              if isinstance(n, EinsumNode) else n for n in program.nodes])
+    """The baseline every lowering is verified against: each contraction annotated to read
+    contiguous operands (``read_mode="NN"``) and store a contiguous result (``fuse_out=False``)."""
+    nodes = [replace(n, read_mode="NN", fuse_out=False) if isinstance(n, EinsumNode) else n
+             for n in program.nodes]
+    return Program(nodes=nodes, inputs=list(program.inputs), outputs=list(program.outputs))
 
 
-class EnableDirectReads(Transform):
-    """``read_mode`` NN -> auto on every contraction: contract strided views without copying
-    them first."""
+class AnnotationLever(Transform):
+    """Set one EinsumNode annotation ``field`` from ``before`` to ``after`` wherever it holds
+    ``before``."""
+    stage = "annotation"
+    field: str = ""
+    before: Any = None
+    after: Any = None
+    no_site_note = "every contraction already annotated"
+
+    def sites(self, flow: Dataflow) -> List[int]:
+        return flow.find(lambda n: isinstance(n, EinsumNode)
+                         and getattr(n, self.field) == self.before)
+
+    def rewrite(self, flow: Dataflow, site: int, edit: ProgramEdit) -> str:
+        edit.replace([site], [replace(flow.nodes[site], **{self.field: self.after})])
+        return ""
+
+    def apply(self, program: Program) -> TransformResult:
+        res = super().apply(program)
+        if res.changed:
+            res.note = f"{res.sites} contraction(s): {self.field} {self.before!r} -> {self.after!r}"
+        return res
+
+
+class EnableDirectReads(AnnotationLever):
     name = "enable-direct-reads"
-    summary = "EinsumNode read_mode NN -> auto (contract views directly)"
-
-    def match(self, program: Program) -> int:
-        return sum(isinstance(n, EinsumNode) and n.read_mode == "NN" for n in program.nodes)
-
-    def apply(self, program: Program) -> TransformResult:
-        sites, nodes = 0, []
-        for n in program.nodes:
-            if isinstance(n, EinsumNode) and n.read_mode == "NN":
-                n = replace(n, read_mode="auto")
-                sites += 1
-            nodes.append(n)
-        return TransformResult(_rebuild(program, nodes), sites > 0, sites,
-                               f"{sites} einsum(s) -> direct read")
+    summary = "contraction read_mode NN -> auto (operands read as they lie)"
+    field, before, after = "read_mode", "NN", "auto"
 
 
-class EnableFusedStore(Transform):
-    """``fuse_out`` False -> True on every contraction: a permuted result may stay a view."""
+class EnableFusedStore(AnnotationLever):
     name = "enable-fused-store"
-    summary = "EinsumNode fuse_out False -> True (permuted result kept as a view)"
-
-    def match(self, program: Program) -> int:
-        return sum(isinstance(n, EinsumNode) and not n.fuse_out for n in program.nodes)
-
-    def apply(self, program: Program) -> TransformResult:
-        sites, nodes = 0, []
-        for n in program.nodes:
-            if isinstance(n, EinsumNode) and not n.fuse_out:
-                n = replace(n, fuse_out=True)
-                sites += 1
-            nodes.append(n)
-        return TransformResult(_rebuild(program, nodes), sites > 0, sites,
-                               f"{sites} einsum(s) -> fused store permitted")
+    summary = "contraction fuse_out False -> True (result may keep the consumer's layout)"
+    field, before, after = "fuse_out", False, True

@@ -9,12 +9,13 @@ matches are the builder's documented contract.
 """
 from __future__ import annotations
 
-from typing import List, Optional, Tuple
+from typing import List, Tuple
 
 import torch
 
-from ..ir import EinsumNode, FusedNode, Node, Program, TensorOp, VecGlueNode, node_outputs
-from ..transform import Transform, TransformResult, producer_index, splice
+from ..dataflow import Dataflow, ProgramEdit
+from ..ir import EinsumNode, FusedNode, Node, Program, TensorOp, VecGlueNode
+from ..transform import Transform
 
 
 def has_fused(program: Program, kernel_prefix: str) -> bool:
@@ -39,26 +40,24 @@ class _ResidentScan(Transform):
         self.M = B * H * nc
         self.work = work
 
-    def _region(self, program: Program) -> Optional[Tuple[set, int]]:
+    stage = "structural"
+    no_site_note = "no canonical scan region"
+
+    def sites(self, flow: Dataflow) -> List[set]:
+        """The unrolled scan's steps (one site): every step binding a name of the canonical
+        scan region, found by the builder's documented names."""
+        program = flow.program
         if has_fused(program, "chunk_h_scan") or self.family_input not in program.inputs:
-            return None
-        prod = producer_index(program)
-        if not all(n in prod for n in ("S0", "h_flat", "vn_flat")):
-            return None
+            return []
+        if not all(flow.producer(n) is not None for n in ("S0", "h_flat", "vn_flat")):
+            return []
         names = {"S0", "h_bh", "h_flat", "vn_bh", "vn_flat"}
         for c in range(self.nc):
             names.update(p.format(c=c, c1=c + 1) for p in self.per_chunk)
-        drop = {i for i, n in enumerate(program.nodes) if any(o in names for o in node_outputs(n))}
-        return (drop, min(drop)) if drop else None
+        steps = {i for n in names if (i := flow.producer(n)) is not None}
+        return [steps] if steps else []
 
-    def match(self, program: Program) -> int:
-        return 1 if self._region(program) is not None else 0
-
-    def apply(self, program: Program) -> TransformResult:
-        region = self._region(program)
-        if region is None:
-            return TransformResult(program, False, 0, "no canonical scan region")
-        drop, at = region
+    def rewrite(self, flow: Dataflow, steps: set, edit: ProgramEdit) -> str:
         B, H, nc, C, D, M = self.B, self.H, self.nc, self.C, self.D, self.M
         new: List[Node] = [VecGlueNode("mul", ["kb5", self.k_coef], self.k_scaled,
                                        out_dtype=self.work)]
@@ -79,8 +78,8 @@ class _ResidentScan(Transform):
         new.append(EinsumNode("nid,nde->nie", ["W_m", "h_flat"], "WS_all", out_dtype=self.work,
                               read_mode="NN", fuse_out=False))
         new.append(VecGlueNode("sub", ["U_m", "WS_all"], "vn_flat", out_dtype=self.work))
-        return TransformResult(splice(program, drop, at, new), True, 1,
-                               f"scan of {nc} chunks -> chunk_h_scan (state in registers)")
+        edit.replace(steps, new)
+        return f"scan of {nc} chunks -> chunk_h_scan (state in registers)"
 
 
 class LowerResidentScan(_ResidentScan):

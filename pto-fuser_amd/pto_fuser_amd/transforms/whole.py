@@ -36,6 +36,7 @@ _NATIVE = ("qF", "kF", "vF", "g_native", "beta_native")
 class _WholeForward(Transform):
     family_input = ""
     kernel = ""
+    stage = "whole"
 
     def __init__(self, B: int, H: int, nc: int, C: int, D: int,
                  work: torch.dtype = torch.bfloat16) -> None:

@@ -82,18 +82,23 @@ def _flash_perdim(inputs, params):
     return [torch.from_numpy(L @ _np(v).reshape(M, C, D)).float()]
 
 
+def _cpu(fn, *slots) -> _Recipe:
+    """A library-free recipe (empty src_file): the launch ignores lib and ws."""
+    return _Recipe(src_dir="", src_file="", defines=lambda p: dict(p), setup_sym="",
+                   teardown_sym="", bind=lambda lib: None,
+                   launch=lambda lib, ws, inputs, params: fn(inputs, params),
+                   contract=FusedContract(list(slots), [], [], torch.float32, "CPU stand-in"))
+
+
 def cpu_fused_registry() -> FusedKernelRegistry:
     reg = FusedKernelRegistry()
-    c = lambda *slots: FusedContract(list(slots), [], [], torch.float32, "CPU stand-in")
-    key = lambda p: dict(p)
-    reg.register("chunk_h_scan", _Recipe("cpu", key, _scan, c("w", "u", "k", "decay")))
+    reg.register("chunk_h_scan", _cpu(_scan, "w", "u", "k", "decay"))
     for s in ("", "_v2"):
-        reg.register("kkt_gated_native" + s, _Recipe("cpu", key, _kkt_native, c("k", "g", "b")))
-        reg.register("gated_qk_native" + s, _Recipe("cpu", key, _qk_native, c("a", "b", "g", "b")))
-        reg.register("qk_prologue" + s, _Recipe("cpu", key, _prologue, c("q", "k", "P", "iP")))
-        reg.register("qkv_flash_native" + s, _Recipe("cpu", key, _flash, c("q", "k", "v", "g", "b")))
-        reg.register("qkvp_flash_native" + s,
-                     _Recipe("cpu", key, _flash_perdim, c("q", "k", "v", "a", "b")))
+        reg.register("kkt_gated_native" + s, _cpu(_kkt_native, "k", "g", "b"))
+        reg.register("gated_qk_native" + s, _cpu(_qk_native, "a", "b", "g", "b"))
+        reg.register("qk_prologue" + s, _cpu(_prologue, "q", "k", "P", "iP"))
+        reg.register("qkv_flash_native" + s, _cpu(_flash, "q", "k", "v", "g", "b"))
+        reg.register("qkvp_flash_native" + s, _cpu(_flash_perdim, "q", "k", "v", "a", "b"))
     return reg
 
 

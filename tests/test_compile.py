@@ -37,7 +37,7 @@ def test_cost_predictions_worth_trying():
     cm, f = CostModel(), Features(1, 16, 8, 128, 128)
     for name in ("enable-direct-reads", "enable-fused-store", "lower-resident-scan",
                  "lower-perdim-scan", "fuse-contraction-epilogue", "fuse-chunk-o-flash",
-                 "fuse-perdim-chunk-o-flash", "batch-chunk-intra-score"):
+                 "fuse-perdim-chunk-o-flash", "fuse-gdn-forward", "fuse-kda-forward"):
         assert cm.predict(name, f).worth_trying, name
     assert not cm.predict("unknown", f).worth_trying
 

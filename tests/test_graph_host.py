@@ -1,52 +1,79 @@
-"""Graph-replay and fusion-decision host contracts (no device) — reference tests/test_graph.py
-and the FusionDecision part of tests/test_fusion.py."""
-import pytest
+"""Host-side contracts of graph recording and fusion decisions (no device).
 
-from pto_fuser_amd import FusionDecision, GraphReplayExecutor, capture_mode, format_fusion_decisions
+capture_mode counts nesting depth; the recording executor runs every step inside it; replay
+refuses to run without a graph; a FusionDecision's verdicts are derived from its measurements
+and cannot disagree with them."""
+import pytest
+import torch
+
+from cpu_kernels import cpu_fused_registry
+from pto_fuser_amd import (CaptureExecutor, FusionDecision, GraphReplayExecutor, OpaqueContract,
+                           OpaqueNode, OpaqueRegistry, Program, capture_mode,
+                           format_fusion_decisions)
 from pto_fuser_amd import registry as reg
 
 
-def test_capture_mode_toggles_and_restores():
-    assert reg._CAPTURE_MODE is False
-    with capture_mode():
-        assert reg._CAPTURE_MODE is True and reg.in_capture_mode()
-    assert reg._CAPTURE_MODE is False
-
-
-def test_capture_mode_restores_on_exception():
-    with pytest.raises(RuntimeError):
-        with capture_mode():
-            raise RuntimeError("boom")
-    assert reg._CAPTURE_MODE is False
-
-
-def test_capture_mode_nests():
+def test_capture_mode_depth():
+    assert not reg.in_capture_mode()
     with capture_mode():
         with capture_mode():
-            assert reg._CAPTURE_MODE is True
-        assert reg._CAPTURE_MODE is True
-    assert reg._CAPTURE_MODE is False
+            assert reg.in_capture_mode()
+        assert reg.in_capture_mode()          # leaving the inner region keeps the outer one
+    assert not reg.in_capture_mode()
 
 
-def test_replay_before_capture_raises():
-    with pytest.raises(RuntimeError, match="capture()"):
+def test_capture_mode_unwinds_on_error():
+    with pytest.raises(KeyError):
+        with capture_mode():
+            with capture_mode():
+                raise KeyError("x")
+    assert not reg.in_capture_mode()
+
+
+def test_recording_executor_runs_steps_in_capture_mode():
+    seen = []
+    opaque = OpaqueRegistry()
+    opaque.register("probe", factory=lambda: None,
+                    lowering=lambda raw, ins, p: seen.append(reg.in_capture_mode()) or ins[0] * 2,
+                    contract=OpaqueContract([torch.float32], torch.float32))
+    prog = Program([OpaqueNode("probe", ["x"], "y")], ["x"], ["y"])
+    out = CaptureExecutor(opaque, fused=cpu_fused_registry()).run(prog, {"x": torch.ones(3)})
+    assert seen == [True] and torch.equal(out["y"], torch.full((3,), 2.0))
+    assert not reg.in_capture_mode()
+
+
+def test_replay_needs_a_graph():
+    with pytest.raises(RuntimeError, match="capture"):
         GraphReplayExecutor().replay({})
 
 
-def test_decision_kept_only_if_gated_det_and_faster():
-    keep = FusionDecision("s", "k", gated_ok=True, deterministic=True, faster=True, kept=True,
-                          t_staged_ms=1.0, t_fused_ms=0.5, frob=0.0, detail="")
-    assert keep.kept and abs(keep.speedup - 2.0) < 1e-9 and "FUSE" in str(keep)
-    drop = FusionDecision("s", "k", gated_ok=True, deterministic=False, faster=True, kept=False,
-                          t_staged_ms=1.0, t_fused_ms=0.5, frob=0.0, detail="")
-    assert not drop.kept and "stage" in str(drop)
-    assert "1/2 stages fused" in format_fusion_decisions([keep, drop])
+@pytest.mark.parametrize("frob,det,staged,fused,kept,why", [
+    (1e-4, True, 1.0, 0.5, True, "kept"),
+    (5e-2, True, 1.0, 0.5, False, "frob"),
+    (1e-4, False, 1.0, 0.5, False, "runs differ"),
+    (1e-4, True, 0.5, 1.0, False, "not faster"),
+    (5e-2, False, 0.5, 1.0, False, "frob"),
+])
+def test_decision_verdict_is_derived(frob, det, staged, fused, kept, why):
+    d = FusionDecision("stage", "kernel", frob, det, staged, fused)
+    assert d.kept is kept and why in d.detail
+    assert d.speedup == pytest.approx(staged / fused)
+    assert str(d).startswith("FUSE" if kept else "stage")
+
+
+def test_decision_summary_counts_kept():
+    ds = [FusionDecision("a", "k", 0.0, True, 2.0, 1.0), FusionDecision("b", "k", 0.0, True, 1.0, 2.0),
+          FusionDecision("c", "k", 0.0, True, 3.0, 1.0, tol=0.0)]
+    text = format_fusion_decisions(ds)
+    assert text.splitlines()[-1].startswith("1/3 stages fused")
+    assert len(text.splitlines()) == 4
 
 
 def test_opaque_registry_contract():
     r = reg.default_registry()
     assert r.keys() == ["tri_inv_rec_unroll"]
-    with pytest.raises(ValueError):
+    assert r.contract("tri_inv_rec_unroll").out_dtype == torch.float32
+    with pytest.raises(ValueError, match="already registered"):
         r.register("tri_inv_rec_unroll", factory=None, lowering=None, contract=None)
-    with pytest.raises(KeyError):
+    with pytest.raises(KeyError, match="tri_inv_rec_unroll"):
         r.run("nope", [], {})

@@ -10,14 +10,13 @@ import torch
 
 from cpu_kernels import cpu_fused_registry, cpu_opaque_registry
 from oracle.gdn_oracle import deltanet_reference, gdn_reference, kda_reference, max_rel
-from pto_fuser_amd import (EinsumNode, Features, FusedNode, Program, StagedExecutor, TensorOp,
-                           VecGlueNode, canonicalize, compile_program)
+from pto_fuser_amd import Features, FusedNode, StagedExecutor, canonicalize, compile_program
 from pto_fuser_amd.forwards import (build_deltanet_program, build_gdn_program, build_kda_program,
                                     build_scan_fused_program, build_scan_staged_program,
                                     make_gdn_inputs, make_inputs, make_kda_inputs,
                                     make_scan_inputs, prepare_gdn_bindings, prepare_kda_bindings)
 from pto_fuser_amd.template import FuseChunkOFlash, FuseContractionEpilogue
-from pto_fuser_amd.transforms import BatchChunkIntraScore, LowerResidentScan
+from pto_fuser_amd.transforms import LowerResidentScan
 
 F32 = torch.float32
 B, H, nc, C, D = 2, 2, 3, 16, 32
@@ -103,40 +102,6 @@ def test_scan_stage_programs_agree(perdim):
     for n in ("h_out", "final"):
         assert a[n].shape == b[n].shape
         assert max_rel(_np(b[n]), _np(a[n])) < 1e-5
-
-
-def _chunked_program(N, ncc, Cc, Dd):
-    """A minimal chunked-linear program: per chunk tril(q_c·k_cᵀ)·v_c, summed into o."""
-    nodes, outs = [], []
-    for c in range(ncc):
-        for x in ("q", "k", "v"):
-            nodes.append(TensorOp("slice", [x], f"{x}{c}", {"axis": 1, "index": c}))
-        nodes.append(EinsumNode("nid,njd->nij", [f"q{c}", f"k{c}"], f"s{c}", out_dtype=F32))
-        nodes.append(VecGlueNode("tril", [f"s{c}"], f"A{c}", {"diagonal": 0}, out_dtype=F32))
-        nodes.append(EinsumNode("nij,nje->nie", [f"A{c}", f"v{c}"], f"o{c}", out_dtype=F32))
-        outs.append(f"o{c}")
-    nodes.append(TensorOp("stack", outs, "o", {"dim": 1}))
-    return Program(nodes, ["q", "k", "v", "P", "invP", "g_intra", "beta_intra"], ["o"])
-
-
-def test_batch_chunk_intra_score_scalar_gate():
-    N, ncc, Cc, Dd = 3, 4, 16, 32
-    gen = torch.Generator().manual_seed(5)
-    binds = {x: torch.randn(N, ncc, Cc, Dd, generator=gen) for x in ("q", "k", "v")}
-    binds.update(P=torch.ones(N, ncc, Cc, Dd), invP=torch.ones(N, ncc, Cc, Dd),
-                 g_intra=torch.zeros(N, ncc, Cc), beta_intra=torch.ones(N, ncc, Cc))
-    prog = _chunked_program(N, ncc, Cc, Dd)
-    t = BatchChunkIntraScore(N, ncc, Cc, Dd, Dd)
-    assert t.match(prog) == 1
-    low = t.apply(prog).program
-    fused = [n for n in low.nodes if isinstance(n, FusedNode)]
-    assert len(fused) == 1 and fused[0].kernel == "gated_qk_native_v2"
-    assert t.match(low) == 0
-    ex = _exec()
-    assert max_rel(_np(ex.run(low, binds)["o"]), _np(ex.run(prog, binds)["o"])) < 1e-5
-    pd = BatchChunkIntraScore(N, ncc, Cc, Dd, Dd, per_dim_gate=True).apply(prog).program
-    assert {n.kernel for n in pd.nodes if isinstance(n, FusedNode)} == {"qk_prologue"}
-    assert max_rel(_np(ex.run(pd, binds)["o"]), _np(ex.run(prog, binds)["o"])) < 1e-5
 
 
 def test_product_registries_refuse_cpu_tensors():

@@ -7,6 +7,7 @@ from pto_fuser_amd import Features, FusedNode, Policy, canonicalize, compile_pro
 from pto_fuser_amd.forwards import (KDA_PROGRAM_INPUTS, build_deltanet_program, build_gdn_program,
                                     build_kda_program, make_gdn_inputs, make_kda_inputs,
                                     prepare_gdn_bindings, prepare_kda_bindings)
+from pto_fuser_amd import _build
 from pto_fuser_amd.fused import _per_token_gate, default_fused_registry
 from pto_fuser_amd.transforms import FuseGdnForward, FuseKdaForward
 
@@ -93,11 +94,15 @@ def test_whole_forward_after_a_stage_lowering_still_matches():
 
 def test_registry_whole_forward_contracts():
     reg = default_fused_registry()
-    for key, entry in (("gdn_forward", "pf_gdn_exec"), ("kda_forward", "pf_kda_exec")):
+    for key in ("gdn_forward", "kda_forward"):
         c = reg.contract(key)
         assert c.in_slots == ["q", "k", "v", "g_native", "beta_native"]
         assert c.out_names == ["o"] and c.out_dtype == torch.float32
-        assert reg.kernel(key, {"B": 1, "H": 2, "nc": 2, "C": 64, "D": 128}).entry == entry
+        r = reg.recipe(key)
+        assert r.src_file == _build.LIB_NAME and r.src_dir == _build.LIB_DIR
+        assert r.setup_sym == "" and r.teardown_sym == ""     # workspaces live in the ops module
+        assert r.defines({"B": 1, "H": 2, "nc": 2, "C": 64, "D": 128, "x": 0}) == \
+            {"B": 1, "H": 2, "nc": 2, "C": 64, "D": 128}
 
 
 def test_bindings_carry_the_fp32_cumulative_gates():
