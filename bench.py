@@ -4,24 +4,28 @@
 Contract: ``python bench.py --gpus N --steps K --warmup W`` prints ONE JSON line.  A step is
 one full forward of the headline workload (B=4, H=16, T=4096, C=64, dk=dv=128, bf16 inputs,
 fp32 accumulation/state/output) through the C-ABI library: stage 1 (chunk-local gates, kkt,
-(I+A)^-1, gated qk^T) and stage 2 (state scan fused with the output).  Inputs are resident in
-HBM before timing starts; outputs and the workspace are preallocated, so the timed region is
-launches only.  ``value`` is tokens/s = B*T*K / t over exactly K steps bracketed by
-``torch.cuda.synchronize()``, with nothing else recorded inside the loop.
+(I+A)^-1) and stage 2 (the state scan fused with the output; it forms the gated causal score
+q k^T from the q and k rows it stages).  Inputs are resident in HBM before timing starts; outputs
+and the workspace are preallocated, so the timed region is launches only.  ``value`` is tokens/s
+= B*T*K / t over exactly K steps: one HIP event pair on the launch stream brackets the K steps,
+after a synchronize, with nothing else recorded inside the loop, and one synchronize follows.
 
 Order of one run: the CPU baseline (a child process, before this process touches the GPU); a
-256 MiB device-copy rate (a practical HBM ceiling measured in the same run); W warmup steps; the K
-timed steps; then a separate pass of ``--event-steps`` forwards with HIP events around each
-kernel on the launch stream, which gives the per-kernel durations; then the secondary
-configurations.
+256 MiB device-copy rate (a practical HBM ceiling measured in the same run); ``settle_s`` seconds
+of untimed forwards (the GPU's clocks ramp over the first fraction of a second: without it a
+20-step loop measured up to 15 % slower than a 200-step one); W warmup steps; the K timed steps;
+then ``--event-steps`` forwards and as many stage-1 launches, each back to back under one event
+pair on the launch stream, which give the per-kernel durations (stage 1 its loop's average,
+stage 2 the forward's average minus stage 1's; they agree with the rocprofv3 kernel-trace
+averages); then the secondary configurations.
 
 Besides the required fields the line carries:
   * ``roofline`` — the dominant kernel (stage 2) against the MI355X HBM peak.  ``achieved`` is
     the forward's compulsory bytes (q, k, v, beta, g in, o and the final state out: 83 456 B per
     64-token chunk x 4096 chunks = 341.8 MB) over the kernel's event-timed average duration:
     stage 2 reads every input the forward needs and writes o and the state.  ``own_*`` are the
-    same figures on the bytes stage 2 itself moves (it also reads T, P and G from stage 1's
-    workspace: 98 816 B per chunk + the final state).  ``traffic`` is the counter-measured HBM
+    same figures on the bytes stage 2 itself moves (it also reads T and G from stage 1's
+    workspace: 90 624 B per chunk + the final state).  ``traffic`` is the counter-measured HBM
     bytes per launch recorded in profiles/hbm_traffic_gdn_forward.json, reported only when that
     record was taken from the library built from the current sources (its source hash), else
     null;
@@ -50,6 +54,7 @@ sys.path.insert(0, os.path.join(ROOT, "pto-fuser_amd"))
 sys.path.insert(0, ROOT)
 
 WORKLOAD = dict(B=4, H=16, T=4096, C=64, DK=128, DV=128)
+SETTLE_S = 1.0      # untimed GPU work before the warmup steps (clock ramp)
 PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
 PEAK_BF16 = 2.5e15         # dense bf16 MFMA, flop/s
 PEAK_FP32 = 157.3e12       # dense fp32 MFMA, flop/s
@@ -74,6 +79,71 @@ def measured_traffic(kernel, lib_hash):
     return int(sum(kib[c] * rec["scale"][c] * 1024 for c in ("FETCH_SIZE", "WRITE_SIZE")))
 
 
+def _counter_key(name, grid):
+    """Record key of a dispatch in the counter passes: the headline's two kernels (the 32-column
+    scan and the 4096-chunk stage 1) and the KDA secondary's two; None for anything else (the
+    other secondaries, the calibration copies)."""
+    W = WORKLOAD
+    M = W["B"] * W["H"] * W["T"] // W["C"]
+    if "scan_split_kernel<64, 128, 128, 2," in name:
+        return "scan_output"
+    if "chunk_local_kernel" in name and "DF16b" in name and grid == M * 256:
+        return "chunk_local"
+    for k in ("kda_scan", "kda_local"):
+        if k in name:
+            return k
+    return None
+
+
+def summarize_counters(fetch_db, write_db, lib_hash, copy_mib, out=None):
+    """Write the counter record bench.py reads (``COUNTERS``) from two rocprofv3 --pmc runs of
+    ``bench.py --calibrate-copy MIB`` (FETCH_SIZE, then WRITE_SIZE): mean KiB per dispatch of each
+    kernel, the factor that maps a plain copy's counter reading to its true bytes, and the model
+    bytes of the headline kernels, tagged with the library's source hash."""
+    import sqlite3
+    import statistics
+    per, copy = {}, {}
+    for counter, db in (("FETCH_SIZE", fetch_db), ("WRITE_SIZE", write_db)):
+        con = sqlite3.connect(db)
+        rows = con.execute("select kernel_name, grid_size, value from counters_collection "
+                           "where counter_name=?", (counter,)).fetchall()
+        con.close()
+        vals = {}
+        for name, grid, v in rows:
+            if "copyBuffer" in name:
+                copy.setdefault(counter, []).append(v)
+                continue
+            key = _counter_key(name, grid)
+            if key is not None:
+                vals.setdefault(key, []).append(v)
+        for key, v in vals.items():
+            per.setdefault(key, {})[counter] = round(statistics.mean(v), 2)
+            per[key]["dispatches"] = len(v)
+    # the largest copies are the calibration ones (torch's own small copies read far less)
+    copy_kib = max(copy["FETCH_SIZE"]), max(copy["WRITE_SIZE"])
+    calib = copy_mib * 1024
+    model = stage_model(**{k: WORKLOAD[k] for k in ("B", "H", "T", "C", "DK", "DV")}, esize=2)
+    kda = kda_model(**KDA_WORKLOAD)
+    model_bytes = {k: model[k]["bytes"] for k in model if k in per}
+    model_bytes.update({k: kda[k] for k in ("kda_local", "kda_scan") if k in per})
+    rec = {"workload": "GDN forward B4 H16 T4096 C64 dk=dv=128, bf16 in (bench.py headline); KDA "
+                       "forward B2 H32 T8192 (bench.py kda_config5)",
+           "source_hash": lib_hash,
+           "commands": [f"rocprofv3 --pmc {c} -d <dir> -o <name> -- python bench.py --steps 3 "
+                        f"--warmup 1 --no-cpu-baseline --event-steps 1 --calibrate-copy {copy_mib}"
+                        for c in ("FETCH_SIZE", "WRITE_SIZE")],
+           "scale": {"FETCH_SIZE": round(calib / copy_kib[0], 5),
+                     "WRITE_SIZE": round(calib / copy_kib[1], 5)},
+           "calibration": {"copy_bytes": calib * 1024, "FETCH_SIZE": copy_kib[0],
+                           "WRITE_SIZE": copy_kib[1]},
+           "kernels": {k: {c: v[c] for c in ("FETCH_SIZE", "WRITE_SIZE")} for k, v in per.items()},
+           "model_bytes": model_bytes,
+           "dispatches_averaged": min(v["dispatches"] for v in per.values())}
+    with open(out or COUNTERS, "w") as f:
+        json.dump(rec, f, indent=1)
+    return rec
+
+
 def compulsory_bytes(B, H, T, DK, DV, esize, h0=False, g_channels=1):
     """What any forward must move: q, k, v (esize bytes each) + beta and g (fp32; g has
     g_channels values per token) in, o (fp32) and the final state (fp32) out, h0 if given."""
@@ -86,23 +156,32 @@ def compulsory_bytes(B, H, T, DK, DV, esize, h0=False, g_channels=1):
 def stage_model(B, H, T, C, DK, DV, esize):
     """Algorithmic flops and HBM bytes per launch of the two kernels.
 
-    Unit = one (b,h) chunk of C tokens; a launch processes M = B*H*T/C units.
-      stage 1 (chunk-local): reads k, q (2*C*DK*e) + g, beta (2*C*4); writes T and P without
-               the upper-right quadrant no kernel reads ((C*C - (C/2)^2)*e each; P's two other
-               upper 16x16 blocks are not written either: 12*256*e) and G (C*4).  flops: k k^T
-               and q k^T (2 * 2*C*C*DK) + inverse (C^3/3).
-      stage 2 (scan+output): reads q, k, v (2*C*DK*e + C*DV*e), T, P (2*C*C*e: the unread
-               quadrant shares its 128-byte lines with the rows' read halves), G, beta (2*C*4);
-               writes o (C*DV*4); plus the final state (DK*DV*4) once per chain.
-               flops: k S, q S, k^T v_new (3 * 2*C*DK*DV) + T r, P v_new (2 * 2*C*C*DV).
+    Unit = one (b,h) chunk of C tokens; a launch processes M = B*H*T/C units.  For bf16 operands
+    the scan forms the causal score P from the q and k rows it stages, so P never goes through
+    HBM; the fp32 path writes P in stage 1 and reads it in stage 2.
+      stage 1 (chunk-local): reads k (C*DK*e; fp32 also q) + g, beta (2*C*4); writes T without
+               the upper-right quadrant no kernel reads ((C*C - (C/2)^2)*e), G (C*4) and, fp32
+               only, P (its lower blocks and the (0,1), (2,3) zero blocks the scan reads).
+               flops: k k^T (2*C*C*DK), fp32 also q k^T, + the inverse (C^3/3).
+      stage 2 (scan+output): reads q, k, v (2*C*DK*e + C*DV*e), T (C*C*e: the unread quadrant
+               shares its 128-byte lines with the rows' read halves) and, fp32 only, P, G, beta
+               (2*C*4); writes o (C*DV*4); plus the final state (DK*DV*4) once per chain.
+               flops: k S, q S, k^T v_new (3 * 2*C*DK*DV) + T r, P v_new (2 * 2*C*C*DV), bf16
+               also the score q k^T (2*C*C*DK).
     """
     M = B * H * (T // C)
+    score_in_scan = esize == 2
     p_blocks = (C // 16) * (C // 16 + 1) // 2 + 2           # lower blocks + (0,1), (2,3)
-    tp_tile = C * C - (C // 2) ** 2                         # T / P elements any kernel reads
-    s1_bytes = 2 * C * DK * esize + 2 * C * 4 + tp_tile * esize + p_blocks * 256 * esize + C * 4
-    s1_flops = 2 * (2 * C * C * DK) + C ** 3 / 3
-    s2_bytes = (2 * C * DK + C * DV) * esize + 2 * C * C * esize + 2 * C * 4 + C * DV * 4
+    t_tile = C * C - (C // 2) ** 2                          # T elements any kernel reads
+    s1_bytes = (1 if score_in_scan else 2) * C * DK * esize + 2 * C * 4 + t_tile * esize + C * 4
+    s1_flops = (1 if score_in_scan else 2) * (2 * C * C * DK) + C ** 3 / 3
+    s2_bytes = (2 * C * DK + C * DV) * esize + C * C * esize + 2 * C * 4 + C * DV * 4
     s2_flops = 3 * (2 * C * DK * DV) + 2 * (2 * C * C * DV)
+    if score_in_scan:
+        s2_flops += 2 * C * C * DK
+    else:
+        s1_bytes += p_blocks * 256 * esize
+        s2_bytes += C * C * esize
     return {
         "chunk_local": {"units": M, "bytes_per_unit": s1_bytes, "flops_per_unit": s1_flops,
                         "bytes": M * s1_bytes, "flops": M * s1_flops},
@@ -139,7 +218,7 @@ def kda_model(B, H, T, C, DK, DV):
     final = B * H * DK * DV * 4
     compulsory = M * (3 * C * DK * 2 + C * DK * 4 + C * 4 + C * DV * 4) + final
     return {"units": M, "bytes_per_unit": s1 + s2, "bytes": M * (s1 + s2) + final,
-            "compulsory_bytes": compulsory}
+            "compulsory_bytes": compulsory, "kda_local": M * s1, "kda_scan": M * s2 + final}
 
 
 def _event_ms(run, steps: int, warmup: int) -> float:
@@ -255,11 +334,15 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--event-steps", type=int, default=30,
-                    help="forwards timed per kernel (HIP events) after the timed loop")
+    ap.add_argument("--event-steps", type=int, default=50,
+                    help="forwards (and stage-1 launches) timed after the timed loop for the "
+                         "per-kernel durations")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true", help="skip the secondary records")
+    ap.add_argument("--summarize-counters", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
+                    help="write the counter record from two rocprofv3 --pmc result databases "
+                         "(FETCH_SIZE, WRITE_SIZE) of a --calibrate-copy run, then exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run three plain device copies of MIB MiB: the "
                          "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -272,6 +355,12 @@ def main(argv=None) -> int:
               f"communication, so per-GPU throughput at N GPUs is the N=1 figure.",
               file=sys.stderr)
         return 2
+    if args.summarize_counters:
+        from pto_fuser_amd import _build
+        rec = summarize_counters(*args.summarize_counters, _build.source_hash(),
+                                 args.calibrate_copy or 256)
+        print(json.dumps({k: rec[k] for k in ("source_hash", "scale", "kernels", "model_bytes")}))
+        return 0
 
     # the CPU baseline first: its child process forks workers, which must not inherit a GPU context
     cpu = None if args.no_cpu_baseline else cpu_baseline(runs=args.cpu_runs)
@@ -317,27 +406,35 @@ def main(argv=None) -> int:
         stage2()
 
     copy_GBps = device_copy_GBps()
+    # settle: keep the GPU busy with untimed forwards for SETTLE_S seconds before the W warmup
+    # steps, so that a short timed loop runs at the clocks a long one reaches (without it, 20
+    # steps measured up to 15 % slower than 200, the GPU still ramping its clocks)
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(50):
+            step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    # the timed loop: one event pair on the launch stream brackets the K steps, one trailing sync
+    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e_start.record(stream)
     for _ in range(args.steps):
         step()
+    e_end.record(stream)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) / args.steps * 1e3
+    ms_per_step = e_start.elapsed_time(e_end) / args.steps
 
-    # per-kernel durations: a separate pass, events on the launch stream around each kernel
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.event_steps)]
-    for e in ev:
-        e[0].record(stream)
-        stage1()
-        e[1].record(stream)
-        stage2()
-        e[2].record(stream)
-    torch.cuda.synchronize()
-    k1_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in ev)
-    k2_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev)
+    # per-kernel durations, after the timed loop: ``--event-steps`` forwards and as many stage-1
+    # launches, each run back to back under one event pair on the launch stream.  Stage 1's
+    # duration is its own loop's average; stage 2's is the forward's average minus stage 1's,
+    # i.e. its share of a forward as the timed loop runs it (an event between the two kernels
+    # would add a few microseconds to each, and stage 2 repeated alone reads a colder T).
+    n_ev = max(1, args.event_steps)
+    fwd_ms = _event_ms(step, n_ev, 2)
+    k1_ms = _event_ms(stage1, n_ev, 2)
+    k2_ms = fwd_ms - k1_ms
 
     model = stage_model(B, H, T, C, DK, DV, esize=2)
     comp = compulsory_bytes(B, H, T, DK, DV, esize=2)
@@ -378,6 +475,7 @@ def main(argv=None) -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": SETTLE_S,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",

@@ -75,8 +75,8 @@ void pf_gdn_teardown(void* ws);
 /* The same forward with no workspace argument and no allocation of any kind: no counterpart in
  * the reference.  It is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation).  Its workspace is a
- * file-scope device array of 68 MiB (bf16: up to 4 285 chunks of 64 tokens, the B4 H16 T4096
- * headline included; fp32: up to 2 159); a larger input returns PF_ERR_SCRATCH and launches
+ * file-scope device array of 40 MiB (bf16: up to 4 964 chunks of 64 tokens, the B4 H16 T4096
+ * headline included; fp32: up to 1 270); a larger input returns PF_ERR_SCRATCH and launches
  * nothing.  The array's device address is looked up once per device on the first call there
  * (make that call outside any graph capture).  Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (different streams, or threads) race; serialise them.  Same
@@ -87,13 +87,15 @@ int pf_gdn_exec_static(const void* q, const void* k, const void* v, const float*
 
 /* The two stages pf_gdn_exec enqueues, exposed so a caller can time or overlap them
  * separately.  Stage 1 (chunk-local, one workgroup per chunk) writes the within-chunk gate
- * cumsum G, T = (I + A)^-1 and the gated causal score P (multiplied by `scale`) into the
- * workspace, and records `scale` there — the work of the reference's kkt_gated_native_v2 +
- * tri_inv_rec_unroll + gated_qk nodes (fused.py:482-517, registry.py:107-127).  Stage 2 (scan +
- * output, state register-resident) reads them, the scale included, and writes o and h_final —
- * the reference's WY einsums, chunk_h_scan and qkv_flash_native_v2 (_gdn_full.py:199-233,
- * scan_lib.cpp:81-99, qkv_fused_lib.cpp:148-165).  Stage 2 must be ordered after stage 1 on the
- * same workspace (same stream, or an event). */
+ * cumsum G and T = (I + A)^-1 into the workspace, and records `scale` there — the work of the
+ * reference's kkt_gated_native_v2 + tri_inv_rec_unroll nodes (fused.py:482-517,
+ * registry.py:107-127); for fp32 operands it also writes the gated causal score P (multiplied by
+ * `scale`, the reference's gated_qk node), which the bf16 stage 2 forms itself from the q and k
+ * rows it stages (q is then not read by stage 1).  Stage 2 (scan + output, state
+ * register-resident) reads them, the scale included, and writes o and h_final — the reference's
+ * WY einsums, chunk_h_scan and qkv_flash_native_v2 (_gdn_full.py:199-233, scan_lib.cpp:81-99,
+ * qkv_fused_lib.cpp:148-165).  Stage 2 must be ordered after stage 1 on the same workspace (same
+ * stream, or an event). */
 int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, const float* g,
                             int B, int H, int T, int C, int DK, int DV, int dtype, float scale,
                             void* ws, void* stream);

@@ -35,14 +35,15 @@ size_t elem_size(int dtype) { return dtype == PF_DTYPE_BF16 ? 2 : 4; }
 bool valid_dtype(int dtype) { return dtype == PF_DTYPE_F32 || dtype == PF_DTYPE_BF16; }
 
 // Byte layout of the fused-forward workspace:
-//   [ T (M*C*C E) | P (M*C*C E, pre-scaled) | G (M*C fp32) | output scale (fp32, 256 B slot) ].
+//   [ T (M*C*C E) | P (M*C*C E, pre-scaled; fp32 only) | G (M*C fp32) | output scale (fp32, 256 B) ].
+// The bf16 scan forms P from the q and k rows it stages, so the bf16 layout has no P.
 struct GdnLayout {
   size_t t_off, p_off, g_off, s_off, total;
   GdnLayout(size_t M, int C, int dtype) {
     const size_t cc = M * C * C * elem_size(dtype);
     t_off = 0;
     p_off = align256(cc);
-    g_off = p_off + align256(cc);
+    g_off = p_off + (dtype == PF_DTYPE_BF16 ? 0 : align256(cc));
     s_off = g_off + align256(M * C * sizeof(float));
     total = s_off + 256;
   }
@@ -65,14 +66,17 @@ void chunk_local_launch(const void* q, const void* k, const float* beta, const f
   a.g = g;
   a.G_out = reinterpret_cast<float*>(base + lay.g_off);
   a.T_out = base + lay.t_off;
-  a.P_out = base + lay.p_off;
+  a.P_out = std::is_same<E, bf16>::value ? nullptr : base + lay.p_off;
   a.A_out = nullptr;
   a.M = static_cast<int>(M);
   a.g_is_cumsum = 0;
   a.t_lower_only = 1;   // the scan kernels read T's rows 0..31 up to column 31 only
   a.p_scale = scale;
   a.scale_out = reinterpret_cast<float*>(base + lay.s_off);
-  pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
+  if constexpr (std::is_same<E, bf16>::value)   // no P: the bf16 scan forms it from its q, k rows
+    pf::chunk_local_kernel<E, E, C, DK, false, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
+  else
+    pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
 }
 
 // CUs of the current device (queried once; 256 on MI355X if the query fails).
@@ -154,10 +158,10 @@ int gdn_check(int B, int H, int T, int C, int DK, int DV, int dtype, const void*
 }
 
 // ---- the allocation-free forward ---------------------------------------------------------
-// Its workspace is this file-scope array, 68 MiB: the bf16 headline shape (B4 H16 T4096, 4096
-// chunks: T, P 32 MiB each, G 1 MiB) fits with room to spare; bf16 up to 4 285 chunks of 64
-// tokens, fp32 up to 2 159.  Every GPU the library runs on holds one copy until the process ends.
-constexpr size_t kStaticScratchBytes = size_t(68) << 20;
+// Its workspace is this file-scope array, 40 MiB: the bf16 headline shape (B4 H16 T4096, 4096
+// chunks: T 32 MiB, G 1 MiB) fits with room to spare; bf16 up to 4 964 chunks of 64 tokens, fp32
+// (T and P) up to 1 270.  Every GPU the library runs on holds one copy until the process ends.
+constexpr size_t kStaticScratchBytes = size_t(40) << 20;
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 // Device address of `scratch` on the current device, resolved once per device with

@@ -2,7 +2,8 @@
 // chunk's work split over four MFMA waves (one per SIMD) by token block and state row block.
 //
 // Workgroup = one chain bh x one slice of NCOL = 16*NT state columns.  Per chunk c (C = 64, DK =
-// 128), with T = (I+A)^-1, the pre-scaled causal score P and G from stage 1:
+// 128), with T = (I+A)^-1 and G from stage 1 and the gated causal score
+// P = scale causal_incl(q k^T ⊙ e^{min(G_i - G_j, 0)}) formed here:
 //
 //   Y = k S,  r = beta v - beta e^G Y,  v_new = T r,
 //   o = scale e^G (q S) + P v_new,  S <- e^{G_last} S + k^T (v_new e^{G_last - G}).
@@ -24,15 +25,18 @@
 //
 // Three workgroup barriers per chunk: after RX is written (B1), after VX / VXs (B2), after the
 // state is published and the chunk's stage buffer released (B3).  Per wave and chunk: 16 MFMAs
-// for k S and q S, 2 or 4 for T r, 2 or 4 for P v_new, 8 for the update (NT = 2) — against 64
-// for one wave holding 16 columns through the whole chain.
+// for k S and q S, 2 or 4 for T r, 2 or 4 for P v_new, 8 for the update (NT = 2), and 8 or 12
+// for the score: its ten 16x16 tiles (4 MFMAs each) are formed in phase B from the staged k and
+// q rows, three, three, two and two per wave so that the phase carries the same number of
+// products on every wave; the tiles (2,0), (3,0) and (3,1) reach their owners through PX.  P
+// never goes through HBM, and stage 1 reads no q.
 //
 // NLW loader waves (the rest of the workgroup) own the loads: chunk c+3's loads issued while the
 // compute waves work on chunk c (three rotating register sets), and chunk c+1 written into the
 // free half of a double-buffered LDS stage (k and q rows swizzled for the permuted-K operand
-// reads and the transposed k^T reads, T and P rows, the v tile row-major, per-token gate tables).
+// reads and the transposed k^T reads, T rows, the v tile row-major, per-token gate tables).
 // Both are spread over the three phases of the interval (k and q loads and k's LDS rows in the
-// first, T and P in the second, v, the gates and q's rows in the third), and the loader waves run
+// first, T in the second, v, the gates and q's rows in the third), and the loader waves run
 // at the default wave priority: a burst of loads or LDS writes issued at once, or at a raised
 // priority, was measured to stall the compute waves sharing the SIMDs (one phase lost up to
 // 1 000 cycles).  The compute waves store their o rows themselves, one 16-byte store per lane and
@@ -50,13 +54,13 @@ namespace pf {
 template <int C, int DK, int NCOL>
 struct SplitStage {
   static constexpr int KP = DK + 16;   // k, q rows: Swz<2,3>
-  static constexpr int TP = C + 8;     // T, P rows: Swz<3,1>
+  static constexpr int TP = C + 8;     // T rows: Swz<3,1>
   static constexpr int VP = NCOL + 8;  // v tile rows (bf16, row-major)
   bf16 ks[C * KP];
   bf16 qs[C * KP];
   bf16 ts[C * TP];
-  bf16 ps[C * TP];
   bf16 vs[C * VP];
+  float GT[C];    // G_t (within-chunk cumulative log decay)
   float BT[C];    // beta_t
   float BEG[C];   // beta_t e^{G_t} f_c
   float EGS[C];   // scale e^{G_t} f_c
@@ -69,7 +73,7 @@ template <int NLW, int NCOL>
 struct SplitRegs {
   static constexpr int NK = 1024 / (64 * NLW), NTP = 512 / (64 * NLW);
   static constexpr int NV = (8 * NCOL + 64 * NLW - 1) / (64 * NLW);
-  uint4 k[NK], q[NK], t[NTP], p[NTP], v[NV];
+  uint4 k[NK], q[NK], t[NTP], v[NV];
   float g, b;
 };
 
@@ -90,6 +94,7 @@ void scan_split_kernel(ScanOutArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 RX[2 * NT * FRAG];
   __shared__ __attribute__((aligned(16))) bf16 VX[2 * NT * FRAG];
   __shared__ __attribute__((aligned(16))) bf16 VXs[2 * NT * FRAG];
+  __shared__ __attribute__((aligned(16))) bf16 PX[3 * 64 * 4];   // score tiles (2,0) (3,0) (3,1)
 
   int bh, slice;
   const int bid = blockIdx.x;
@@ -113,7 +118,6 @@ void scan_split_kernel(ScanOutArgs a) {
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(static_cast<const bf16*>(a.q) + (size_t)bh * Tlen * DK, Tlen * DK * 2);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(static_cast<const bf16*>(a.v) + (size_t)bh * Tlen * DV, Tlen * DV * 2);
     const __amdgpu_buffer_rsrc_t rt = make_rsrc(static_cast<const bf16*>(a.Tm) + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(static_cast<const bf16*>(a.P) + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
     const float* Gc = a.G + (size_t)bh * Tlen;
     const float* Bc = a.beta + (size_t)bh * Tlen;
     const float oscale = *a.scale;
@@ -161,7 +165,6 @@ void scan_split_kernel(ScanOutArgs a) {
       for (int i = 0; i < Regs::NTP; ++i) {
         const uint32_t rowi = trow_i(i);
         r.t[i] = buf_load16(rt, tp_voff, tp_s + rowi * C * 2);
-        r.p[i] = buf_load16(rp, tp_voff, tp_s + rowi * C * 2);
       }
     };
     auto load_vg = [&](Regs& r, int ch) {
@@ -187,7 +190,6 @@ void scan_split_kernel(ScanOutArgs a) {
       for (int i = 0; i < Regs::NTP; ++i) {
         const int rowi = trow_i(i);
         put16(s.ts + tp_lds + rowi * TP, r.t[i], (i & 1) != 0);
-        put16(s.ps + tp_lds + rowi * TP, r.p[i], (i & 1) != 0);
       }
     };
     auto store_vg = [&](Stage& s, const Regs& r, int ch) {
@@ -203,6 +205,7 @@ void scan_split_kernel(ScanOutArgs a) {
       const float Lnext = renorm ? 0.f : Ln;
       if (lt < C) {
         const float eg = __expf(r.g + Lrun);
+        s.GT[lt] = r.g;
         s.BT[lt] = r.b;
         s.BEG[lt] = r.b * eg;
         s.EGS[lt] = oscale * eg;
@@ -276,7 +279,9 @@ void scan_split_kernel(ScanOutArgs a) {
     // per-lane LDS element offsets
     const int kq_rd = (tok0 + c) * KP + 4 * (g ^ ((c >> 2) & 3));          // k / q rows
     const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g) + 32 * cw; // k^T, rows 32cw..
-    const int tp_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // T / P rows
+    const int tp_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // T rows
+    const int kj_rd = c * KP + 4 * (g ^ ((c >> 2) & 3));                   // k / q rows 16 b + c
+    const float oscale = *a.scale;
     const int v_rd = (tok0 + 4 * g + (c >> 2)) * VP + 4 * (c & 3);         // v, transposed read
     const int frag = lane * 8;                                             // lane's exchange slot
     const int xhalf = 4 * (cw & 1), xblk = cw >> 1;                        // this wave's RX/VX slot
@@ -301,6 +306,7 @@ void scan_split_kernel(ScanOutArgs a) {
       const Stage& s = st[ch & 1];
       // ---- phase A: Y = k S~ and (q S~)^T for this wave's 16 tokens, r -> RX ----
       floatx4 Y[NT], QT[NT];
+      bf16x8 qf[DK / 32];                                 // q rows, kept for the score of phase B
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) { Y[nt] = zero4(); QT[nt] = zero4(); }
 #pragma unroll
@@ -308,12 +314,12 @@ void scan_split_kernel(ScanOutArgs a) {
         const bf16* kp = s.ks + kq_rd + 32 * kb;
         const bf16* qp = s.qs + kq_rd + 32 * kb;
         const bf16x8 ka = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
-        const bf16x8 qa = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+        qf[kb] = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const bf16x8 sb = *reinterpret_cast<const bf16x8*>(SB + (kb * NT + nt) * FRAG + frag);
           Y[nt] = mfma_bf16(ka, sb, Y[nt]);               // (k S~)[t][n]
-          QT[nt] = mfma_bf16(sb, qa, QT[nt]);             // (q S~)^T[n][t]
+          QT[nt] = mfma_bf16(sb, qf[kb], QT[nt]);         // (q S~)^T[n][t]
         }
       }
       {
@@ -357,6 +363,55 @@ void scan_split_kernel(ScanOutArgs a) {
           *reinterpret_cast<bf16x4*>(VXs + (xblk * NT + nt) * FRAG + frag + xhalf) = vs;
         }
       }
+      // The causal score, formed here from the staged k and q rows instead of read from stage 1.
+      // Tile (ib, jb) (query tokens 16 ib .., key tokens 16 jb .., jb <= ib) is P^T = k_jb q_ib^T,
+      // so lane (c, g) holds P[16 ib + c][16 jb + 4 g + ii], and tiles (ib, 2 kb), (ib, 2 kb + 1)
+      // together are the permuted-K B fragment of o^T = v_new^T P^T for key block kb.  Gate and
+      // mask as in stage 1: P[i][j] = scale (q_i . k_j) e^{min(G_i - G_j, 0)} for j <= i.  The ten
+      // tiles are spread three, three, two, two over the waves so that each wave's phase carries
+      // the same number of products; (2,0), (3,0) (wave 0) and (3,1) (wave 1) reach their owners
+      // through PX after B2.
+      bf16x4 ptl[4];                                     // this wave's own tiles (ib = cw)
+      {
+        auto tile = [&](int ib, int jb) -> bf16x4 {
+          floatx4 acc = zero4();
+#pragma unroll
+          for (int kb = 0; kb < DK / 32; ++kb) {
+            const bf16* kp = s.ks + kj_rd + 16 * jb * KP + 32 * kb;
+            const bf16* qp = s.qs + kj_rd + 16 * ib * KP + 32 * kb;
+            const bf16x8 kr = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
+            const bf16x8 qr = ib == cw ? qf[kb] : cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+            acc = mfma_bf16(kr, qr, acc);
+          }
+          const float gi = s.GT[16 * ib + c];
+          const floatx4 gj = *reinterpret_cast<const floatx4*>(s.GT + 16 * jb + 4 * g);
+          bf16x4 out;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const float keep = (jb < ib || c >= 4 * g + ii) ? oscale : 0.f;
+            out[ii] = (bf16)(keep * acc[ii] * __expf(fminf(gi - gj[ii], 0.f)));
+          }
+          return out;
+        };
+        const bf16x4 z4 = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) ptl[jb] = z4;
+        if (cw == 0) {
+          ptl[0] = tile(0, 0);
+          *reinterpret_cast<bf16x4*>(PX + (0 * 64 + lane) * 4) = tile(2, 0);
+          *reinterpret_cast<bf16x4*>(PX + (1 * 64 + lane) * 4) = tile(3, 0);
+        } else if (cw == 1) {
+          ptl[0] = tile(1, 0);
+          ptl[1] = tile(1, 1);
+          *reinterpret_cast<bf16x4*>(PX + (2 * 64 + lane) * 4) = tile(3, 1);
+        } else if (cw == 2) {
+          ptl[1] = tile(2, 1);
+          ptl[2] = tile(2, 2);
+        } else {
+          ptl[2] = tile(3, 2);
+          ptl[3] = tile(3, 3);
+        }
+      }
       lds_barrier();                                     // B2
       // ---- phase C: o^T = v_new^T P^T + scale e^G f (q S~)^T -> HBM; S~ update -> SB ----
       {
@@ -366,8 +421,13 @@ void scan_split_kernel(ScanOutArgs a) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           if (kb == 0 || cw >= 2) {
-            const bf16* pp = s.ps + tp_rd + 32 * kb;
-            const bf16x8 pb = cat8(*reinterpret_cast<const bf16x4*>(pp), *reinterpret_cast<const bf16x4*>(pp + 16));
+            bf16x4 lo = ptl[2 * kb], hi = ptl[2 * kb + 1];
+            if (kb == 0 && cw == 2) lo = *reinterpret_cast<const bf16x4*>(PX + (0 * 64 + lane) * 4);
+            if (kb == 0 && cw == 3) {
+              lo = *reinterpret_cast<const bf16x4*>(PX + (1 * 64 + lane) * 4);
+              hi = *reinterpret_cast<const bf16x4*>(PX + (2 * 64 + lane) * 4);
+            }
+            const bf16x8 pb = cat8(lo, hi);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
               OT[nt] = mfma_bf16(*reinterpret_cast<const bf16x8*>(VX + (kb * NT + nt) * FRAG + frag), pb, OT[nt]);

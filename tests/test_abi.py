@@ -59,10 +59,14 @@ def test_status_strings_and_version(lib):
 
 
 def test_workspace_sizing_contract(lib):
-    # T (bf16) + P (bf16) + G (fp32), each 256-byte aligned, + a 256-byte slot for the scale
+    # bf16: T (bf16) + G (fp32), each 256-byte aligned, + a 256-byte slot for the scale (the
+    # bf16 scan forms P itself); fp32: T + P (fp32) + G + the slot
     M = 4 * 16 * 64
-    want = 2 * ((M * 64 * 64 * 2 + 255) // 256 * 256) + (M * 64 * 4 + 255) // 256 * 256 + 256
+    al = lambda n: (n + 255) // 256 * 256
+    want = al(M * 64 * 64 * 2) + al(M * 64 * 4) + 256
     assert lib.pf_gdn_workspace_bytes(4, 16, 4096, 64, 128, 128, _hip.PF_DTYPE_BF16) == want
+    want32 = 2 * al(M * 64 * 64 * 4) + al(M * 64 * 4) + 256
+    assert lib.pf_gdn_workspace_bytes(4, 16, 4096, 64, 128, 128, _hip.PF_DTYPE_F32) == want32
     # unsupported shapes / dtypes report size 0 and setup refuses them
     assert lib.pf_gdn_workspace_bytes(1, 1, 100, 64, 128, 128, 1) == 0      # T % C != 0
     assert lib.pf_gdn_workspace_bytes(1, 1, 128, 32, 128, 128, 1) == 0      # C != 64

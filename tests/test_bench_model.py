@@ -16,20 +16,22 @@ def test_stage_model_per_chunk_bytes_and_flops():
     m = bench.stage_model(4, 16, 4096, C, DK, DV, 2)
     s1, s2 = m["chunk_local"], m["scan_output"]
     assert s1["units"] == s2["units"] == 4 * 16 * 64
-    # stage 1: k, q (bf16) + g, beta in; T without its upper-right quadrant and 12 P blocks
-    # (bf16), G out
-    tp = C * C - 32 * 32
-    assert s1["bytes_per_unit"] == 2 * C * DK * 2 + 2 * C * 4 + tp * 2 + 12 * 16 * 16 * 2 + C * 4
-    # stage 2: q, k, v, T, P (bf16, whole 128-byte rows) + G, beta in; o (fp32) out; plus the
-    # final state per chain
-    assert s2["bytes_per_unit"] == (2 * C * DK + C * DV) * 2 + 2 * C * C * 2 + 2 * C * 4 + C * DV * 4 == 98816
-    assert s2["bytes"] == 4096 * 98816 + 64 * DK * DV * 4
-    # flops per chunk: kk^T + qk^T + inverse; kS, qS, k^T v_new + T r, P v_new
-    assert s1["flops_per_unit"] == pytest.approx(4 * C * C * DK + C ** 3 / 3)
-    assert s2["flops_per_unit"] == 6 * C * DK * DV + 4 * C * C * DV
-    # fp32 operands double the operand bytes, not the fp32 gate / output bytes
+    # stage 1 (bf16): k + g, beta in; T without its upper-right quadrant (bf16) and G out
+    t = C * C - 32 * 32
+    assert s1["bytes_per_unit"] == C * DK * 2 + 2 * C * 4 + t * 2 + C * 4
+    # stage 2 (bf16): q, k, v, T (bf16, whole 128-byte rows) + G, beta in; o (fp32) out; plus the
+    # final state per chain.  P is formed on the chip.
+    assert s2["bytes_per_unit"] == (2 * C * DK + C * DV) * 2 + C * C * 2 + 2 * C * 4 + C * DV * 4 == 90624
+    assert s2["bytes"] == 4096 * 90624 + 64 * DK * DV * 4
+    # flops per chunk: kk^T + inverse; kS, qS, k^T v_new + T r, P v_new + the score qk^T
+    assert s1["flops_per_unit"] == pytest.approx(2 * C * C * DK + C ** 3 / 3)
+    assert s2["flops_per_unit"] == 6 * C * DK * DV + 4 * C * C * DV + 2 * C * C * DK
+    # fp32 operands double the operand bytes, and P goes through HBM (12 blocks written, read
+    # as whole rows)
     f = bench.stage_model(1, 1, 64, C, DK, DV, 4)
-    assert f["scan_output"]["bytes_per_unit"] - s2["bytes_per_unit"] == (2 * C * DK + C * DV + 2 * C * C) * 2
+    assert f["scan_output"]["bytes_per_unit"] - s2["bytes_per_unit"] == \
+        (2 * C * DK + C * DV + C * C) * 2 + C * C * 4
+    assert f["chunk_local"]["bytes_per_unit"] == 2 * C * DK * 4 + 2 * C * 4 + t * 4 + 12 * 256 * 4 + C * 4
 
 
 def test_compulsory_bytes_of_the_headline():

@@ -58,7 +58,7 @@ def test_static_forward_matches_workspace_forward(dtype):
 
 
 def test_static_forward_refuses_inputs_beyond_its_scratch():
-    B, H, T = 8, 16, 4096                                 # 8192 chunks: past the 68 MiB scratch
+    B, H, T = 8, 16, 4096                                 # 8192 chunks: past the 40 MiB scratch
     announce(f"pf_gdn_exec_static oversized B{B} H{H} T{T}")
     d = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.bfloat16, seed=23, device=DEV)
     o = torch.full((B, H, T, DV), -7.0, device=DEV)
