@@ -55,7 +55,9 @@ const char* pf_source_hash(void);
  *   q, k [B,H,T,DK] dtype; v [B,H,T,DV] dtype; beta, g [B,H,T] fp32 (g = per-token log decay,
  *   summed within each chunk of C tokens by the kernel); h0 [B,H,DK,DV] fp32 or NULL (zero);
  *   o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV] fp32 or NULL.
- *   Supported: C = 64, DK = DV = 128, T % C == 0.
+ *   Supported: C = 64 or 128, DK = DV = 128, T % C == 0.  The kernels run 64-token chunks; C = 128
+ *   (the reference's chunk) is served by them over T / 64 chunks — the chunked forward's result
+ *   does not depend on the chunk size, only the blocking of its arithmetic does.
  * ------------------------------------------------------------------------------------------ */
 size_t pf_gdn_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
 void* pf_gdn_setup(int B, int H, int T, int C, int DK, int DV, int dtype);
@@ -114,7 +116,8 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
  *   q, k [B,H,T,DK] bf16; v [B,H,T,DV] bf16; beta [B,H,T] fp32; g [B,H,T,DK] fp32 (per-token,
  *   per-channel log decay, summed within each chunk of C tokens by the kernel); h0 [B,H,DK,DV]
  *   fp32 or NULL; o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV] fp32 or NULL.
- *   Supported: dtype PF_DTYPE_BF16, C = 64, DK = DV = 128, T % C == 0, T / C >= 2.
+ *   Supported: dtype PF_DTYPE_BF16, C = 64 or 128 (run as 64-token chunks), DK = DV = 128,
+ *   T % C == 0, T >= 128.
  * ------------------------------------------------------------------------------------------ */
 size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
 void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype);

@@ -49,9 +49,16 @@ struct GdnLayout {
   }
 };
 
+// The kernels' chunk: every forward runs 64-token chunks.  A caller's chunk size of 128 (the
+// reference's) is served by the same kernels over T / 64 chunks: the chunked forward's result does
+// not depend on the chunk size (each is an exact regrouping of the token recurrence), so only the
+// blocking of the arithmetic differs; T must then be a multiple of 128, as the caller's chunking
+// implies.
+constexpr int kChunk = 64;
+
 bool gdn_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
-  return B > 0 && H > 0 && T > 0 && C == 64 && DK == 128 && DV == 128 && T % C == 0 &&
-         valid_dtype(dtype);
+  return B > 0 && H > 0 && T > 0 && (C == 64 || C == 128) && DK == 128 && DV == 128 &&
+         T % C == 0 && valid_dtype(dtype);
 }
 
 template <typename E>
@@ -136,14 +143,14 @@ void scan_output_launch(const void* q, const void* k, const void* v, const float
 int gdn_forward_on(char* base, const void* q, const void* k, const void* v, const float* beta,
                    const float* g, const float* h0, float* o, float* h_final, int B, int H, int T,
                    int C, int dtype, float scale, hipStream_t s) {
-  const size_t M = (size_t)B * H * (T / C);
+  const size_t M = (size_t)B * H * (T / kChunk);
   pf::LaunchScope scope;
   if (dtype == PF_DTYPE_BF16) {
     chunk_local_launch<bf16>(q, k, beta, g, scale, base, M, s);
-    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C, base, s);
+    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / kChunk, base, s);
   } else {
     chunk_local_launch<float>(q, k, beta, g, scale, base, M, s);
-    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C, base, s);
+    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / kChunk, base, s);
   }
   return scope.status();
 }
@@ -152,7 +159,7 @@ int gdn_forward_on(char* base, const void* q, const void* k, const void* v, cons
 int gdn_check(int B, int H, int T, int C, int DK, int DV, int dtype, const void* ws) {
   if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
   const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
-  if (!w || !w->base || w->bytes < GdnLayout((size_t)B * H * (T / C), C, dtype).total)
+  if (!w || !w->base || w->bytes < GdnLayout((size_t)B * H * (T / kChunk), kChunk, dtype).total)
     return PF_ERR_WORKSPACE;
   return PF_OK;
 }
@@ -217,7 +224,7 @@ const char* pf_source_hash(void) { return PF_SOURCE_HASH; }
 
 size_t pf_gdn_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype) {
   if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return 0;
-  return GdnLayout((size_t)B * H * (T / C), C, dtype).total;
+  return GdnLayout((size_t)B * H * (T / kChunk), kChunk, dtype).total;
 }
 
 void* pf_gdn_create(void) { return pf::workspace_create(); }
@@ -247,7 +254,7 @@ int pf_gdn_chunk_local_exec(const void* q, const void* k, const float* beta, con
   if (st != PF_OK) return st;
   if (!q || !k || !beta) return PF_ERR_ARG;
   const GdnWorkspace* w = static_cast<const GdnWorkspace*>(ws);
-  const size_t M = (size_t)B * H * (T / C);
+  const size_t M = (size_t)B * H * (T / kChunk);
   hipStream_t s = static_cast<hipStream_t>(stream);
   pf::LaunchScope scope;
   if (dtype == PF_DTYPE_BF16)
@@ -267,10 +274,10 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
   hipStream_t s = static_cast<hipStream_t>(stream);
   pf::LaunchScope scope;
   if (dtype == PF_DTYPE_BF16)
-    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / C,
+    scan_output_launch<bf16>(q, k, v, beta, h0, o, h_final, B * H, T / kChunk,
                              static_cast<char*>(w->base), s);
   else
-    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / C,
+    scan_output_launch<float>(q, k, v, beta, h0, o, h_final, B * H, T / kChunk,
                               static_cast<char*>(w->base), s);
   return scope.status();
 }
@@ -290,7 +297,7 @@ int pf_gdn_exec_static(const void* q, const void* k, const void* v, const float*
                        const float* g, const float* h0, float* o, float* h_final, int B, int H,
                        int T, int C, int DK, int DV, int dtype, float scale, void* stream) {
   if (!gdn_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
-  if (GdnLayout((size_t)B * H * (T / C), C, dtype).total > kStaticScratchBytes)
+  if (GdnLayout((size_t)B * H * (T / kChunk), kChunk, dtype).total > kStaticScratchBytes)
     return PF_ERR_SCRATCH;
   if (!q || !k || !v || !beta || !o) return PF_ERR_ARG;
   int st = PF_OK;

@@ -34,9 +34,13 @@ struct KdaLayout {
 
 // bf16 operands, C = 64, dk = dv = 128, at least two chunks per chain (the scan kernel's loader
 // pipeline is written for NC >= 2).
+// 64-token chunks in the kernels; a caller's chunk size of 128 runs them over T / 64 chunks (the
+// chunked forward's result does not depend on the chunk size), with T a multiple of 128.
+constexpr int kChunk = 64;
+
 bool kda_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
-  return B > 0 && H > 0 && T > 0 && C == 64 && DK == 128 && DV == 128 && T % C == 0 &&
-         T / C >= 2 && dtype == PF_DTYPE_BF16;
+  return B > 0 && H > 0 && T > 0 && (C == 64 || C == 128) && DK == 128 && DV == 128 &&
+         T % C == 0 && T / kChunk >= 2 && dtype == PF_DTYPE_BF16;
 }
 
 }  // namespace
@@ -45,7 +49,7 @@ extern "C" {
 
 size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype) {
   if (!kda_shape_ok(B, H, T, C, DK, DV, dtype)) return 0;
-  return KdaLayout((size_t)B * H * (T / C), C, DK).total;
+  return KdaLayout((size_t)B * H * (T / kChunk), kChunk, DK).total;
 }
 
 void* pf_kda_create(void) { return pf::workspace_create(); }
@@ -73,8 +77,8 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
                 int DV, int dtype, float scale, void* ws, void* stream) {
   if (!kda_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
   const KdaWorkspace* w = static_cast<const KdaWorkspace*>(ws);
-  const size_t M = (size_t)B * H * (T / C);
-  const KdaLayout lay(M, C, DK);
+  const size_t M = (size_t)B * H * (T / kChunk);
+  const KdaLayout lay(M, kChunk, DK);
   if (!w || !w->base || w->bytes < lay.total) return PF_ERR_WORKSPACE;
   if (!q || !k || !v || !beta || !g || !o) return PF_ERR_ARG;
   constexpr int KC = 64, KD = 128;
@@ -110,7 +114,7 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   sa.o = o;
   sa.h_final = h_final;
   sa.BH = B * H;
-  sa.NC = T / C;
+  sa.NC = T / kChunk;
   constexpr int NLW = 4;
   const unsigned grid = (unsigned)(B * H * (KD / 32));
   pf::kda_scan_kernel<KC, KD, KD, NLW><<<dim3(grid), dim3(64 * (2 + NLW)), 0, s>>>(sa);

@@ -433,15 +433,16 @@ def default_fused_registry() -> FusedKernelRegistry:
             in_slots=["q", "k", "v", "g_native", "beta_native"],
             in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
             notes="whole GDN forward: q/k/v [M,C,D] (bf16, or fp32 end to end), cumulative "
-                  "gate g_native and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64, D = 128")))
+                  "gate g_native and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64 or 128, "
+                  "D = 128")))
     reg.register("kda_forward", _hip_recipe(
         "pf_kda_exec", _shape_key("B", "H", "nc", "C", "D"), _kda_forward_launch,
         FusedContract(
             in_slots=["q", "k", "v", "g_native", "beta_native"],
             in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
             notes="whole KDA forward: q/k/v [M,C,D] bf16, per-channel cumulative gate "
-                  "g_native [M,C,D] and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64, "
-                  "D = 128, nc >= 2")))
+                  "g_native [M,C,D] and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64 or "
+                  "128, D = 128, T >= 128")))
     return reg
 
 

@@ -22,7 +22,7 @@ import torch
 
 from . import _hip
 
-SUPPORTED_C = (64,)
+SUPPORTED_C = (64, 128)   # the fused forwards run 64-token chunks; 128 regroups the same chunks
 SUPPORTED_D = (128,)
 
 
@@ -144,7 +144,8 @@ def gdn_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
     q, k [B,H,T,DK] and v [B,H,T,DV] in float32 or bfloat16; beta, g [B,H,T] float32 (g is the
     per-token log decay, summed within chunks by the kernel; None = DeltaNet); h0 [B,H,DK,DV]
     float32 or None.  Returns (o [B,H,T,DV] float32 scaled by ``scale`` (default DK^-1/2),
-    h_final [B,H,DK,DV] float32 or None)."""
+    h_final [B,H,DK,DV] float32 or None).  chunk_size 64 or 128: both run the 64-token kernels
+    (the result does not depend on the chunk size); T must be a multiple of it."""
     if q.dim() != 4:
         raise ValueError(f"q must be [B,H,T,DK], got shape {tuple(q.shape)}")
     B, H, T, DK = q.shape
@@ -190,8 +191,8 @@ def kkt_inverse(k: torch.Tensor, g: Optional[torch.Tensor], beta: torch.Tensor,
     Returns T = (I + A)^-1 [M, C, C] float32 (and A [M, C, C] float32 if ``return_A``)."""
     C = int(chunk_size)
     DK = k.shape[-1]
-    if C not in SUPPORTED_C or DK not in SUPPORTED_D:
-        raise ValueError(f"unsupported shape C={C} DK={DK}")
+    if C != 64 or DK not in SUPPORTED_D:     # T is the per-chunk inverse: its size is C
+        raise ValueError(f"unsupported shape C={C} DK={DK} (C = 64, DK in {SUPPORTED_D})")
     n = k.numel() // DK
     if n % C:
         raise ValueError(f"token count {n} is not a multiple of C={C}")
@@ -370,8 +371,9 @@ def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
     q, k [B,H,T,DK] and v [B,H,T,DV] bfloat16; beta [B,H,T] float32; g [B,H,T,DK] float32 (the
     per-token, per-channel log decay, summed within chunks by the kernel); h0 [B,H,DK,DV]
     float32 or None.  Returns (o [B,H,T,DV] float32 scaled by ``scale`` (default DK^-1/2),
-    h_final [B,H,DK,DV] float32 or None).  At least two chunks per sequence (T >= 2 C); float32
-    operands are served by the staged KDA program (forwards.kda) instead."""
+    h_final [B,H,DK,DV] float32 or None).  chunk_size 64 or 128 (both run 64-token chunks); at
+    least two of them per sequence (T >= 128); float32 operands are served by the staged KDA
+    program (forwards.kda) instead."""
     if q.dim() != 4:
         raise ValueError(f"q must be [B,H,T,DK], got shape {tuple(q.shape)}")
     B, H, T, DK = q.shape
@@ -380,8 +382,9 @@ def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
     if C not in SUPPORTED_C or DK not in SUPPORTED_D or DV not in SUPPORTED_D:
         raise ValueError(f"unsupported shape C={C} DK={DK} DV={DV} "
                          f"(C in {SUPPORTED_C}, DK/DV in {SUPPORTED_D})")
-    if T % C or T // C < 2:
-        raise ValueError(f"T={T} must be a multiple of the chunk size {C} with at least two chunks")
+    if T % C or T // 64 < 2:
+        raise ValueError(f"T={T} must be a multiple of the chunk size {C} and hold at least two "
+                         f"chunks of 64 tokens")
     if q.dtype != torch.bfloat16:
         raise ValueError(f"the fused KDA forward takes bfloat16 operands, got {q.dtype}")
     dev = q.device

@@ -170,6 +170,27 @@ def test_whole_forward_program_matches_oracle_and_staged(family):
     assert frob_rel(o, staged) < TOL
 
 
+@pytest.mark.parametrize("family", ["gdn", "kda"])
+def test_whole_forward_at_the_reference_chunk_128(family):
+    """The reference's compiled_forward shape (examples/attention/gdn.py:75-88: B=1, H=16, nc=8,
+    C=128, D=128) lowers to the fused two-kernel forward (run as 64-token chunks) and matches the
+    oracle chunked at 128 within the bf16 bound; verified and kept by compile_program."""
+    B, H, nc, C, D = 1, 16, 8, 128, 128
+    announce(f"whole-forward program {family} C128 B{B} H{H} nc{nc}")
+    binds, prog, ref = (_gdn if family == "gdn" else _kda)(B, H, nc, C, D, seed=41)
+    f = Features(B, H, nc, C, D, per_dim_gate=family == "kda")
+    res = compile_program(prog, f, policy=Policy(whole_forward=True), bindings=binds, iters=5,
+                          warmup=2)
+    assert [n.kernel for n in res.program.nodes] == [f"{family}_forward"], str(res.report)
+    assert res.report.records[0].kept, str(res.report)
+    o = StagedExecutor().run(res.program, binds)["o"]
+    torch.cuda.synchronize()
+    assert o.shape == (B, H, nc, C, D)
+    err = _frob(o.cpu(), ref)
+    print(f"{family} C128 whole forward vs oracle: frob {err:.2e}")
+    assert err < TOL, err
+
+
 def test_whole_gdn_forward_fp32_program():
     """fp32 work dtype: the whole-forward node runs the fused fp32 path (1e-4 relative)."""
     B, H, nc, C, D = 1, 2, 3, 64, 128

@@ -134,6 +134,31 @@ def test_gdn_bf16_config4_long_context():
     assert max_abs(h, h_ref) <= BF16_TOL / 2, max_abs(h, h_ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gdn_chunk_size_128(dtype):
+    """C = 128 (the reference's chunk) runs the 64-token kernels over T / 64 chunks: against the
+    oracle chunked at 128 within the stated bound, and equal to the C = 64 call bit for bit (the
+    same kernels on the same data)."""
+    B, H, T = 1, 4, 1024
+    announce(f"GDN {dtype} C128 B{B} H{H} T{T} h0")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=dtype, seed=31, h0_std=0.02)
+    d = {n: (None if t is None else t.to(DEV)) for n, t in inp.items()}
+    o128, h128 = gdn_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"],
+                                   chunk_size=128)
+    o64, h64 = gdn_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"])
+    torch.cuda.synchronize()
+    x = as_oracle_inputs(inp)
+    o_ref, h_ref = gdn_reference(x["q"], x["k"], x["v"], x["beta"], x["g"], h0=x["h0"], C=128,
+                                 dtype=np.float64)
+    bf16 = dtype == torch.bfloat16
+    _check(f"GDN {'bf16' if bf16 else 'fp32'} C128 B{B} H{H} T{T} h0", o128.cpu().numpy(),
+           h128.cpu().numpy(), o_ref, h_ref, bf16=bf16)
+    assert torch.equal(o128, o64) and torch.equal(h128, h64)
+    with pytest.raises(ValueError, match="multiple of the chunk size"):
+        gdn_chunk_forward(d["q"][:, :, :192], d["k"][:, :, :192], d["v"][:, :, :192],
+                          d["beta"][:, :, :192], d["g"][:, :, :192], chunk_size=128)
+
+
 def test_gdn_deterministic():
     announce("GDN bf16 determinism B2 H8 T1024")
     inp = make_delta_inputs(2, 8, 1024, kind="gdn", dtype=torch.bfloat16, seed=7)

@@ -57,11 +57,16 @@ def test_whole_forward_matches_only_its_family_and_supported_shapes():
     assert FuseGdnForward(1, 2, 2, 64, 128).match(kda) == 0
     assert FuseKdaForward(1, 2, 2, 64, 128).match(kda) == 1
     assert FuseKdaForward(1, 2, 2, 64, 128).match(gdn) == 0
-    # chunk and head sizes the fused kernels do not run
+    # the reference's 128-token chunk runs on the 64-token kernels; other chunk / head sizes do not
     assert FuseGdnForward(1, 2, 2, 128, 128).match(
-        canonicalize(build_gdn_program(1, 2, 2, 128, 128, SCALE))) == 0
+        canonicalize(build_gdn_program(1, 2, 2, 128, 128, SCALE))) == 1
+    assert FuseGdnForward(1, 2, 2, 32, 128).match(
+        canonicalize(build_gdn_program(1, 2, 2, 32, 128, SCALE))) == 0
     assert FuseGdnForward(1, 2, 2, 64, 64).match(
         canonicalize(build_gdn_program(1, 2, 2, 64, 64, SCALE))) == 0
+    # KDA at C = 128: one 128-token chunk is two kernel chunks
+    assert FuseKdaForward(1, 2, 1, 128, 128).match(
+        canonicalize(build_kda_program(1, 2, 1, 128, 128, SCALE))) == 1
     # the fused KDA forward takes bf16 operands and at least two chunks
     assert FuseKdaForward(1, 2, 2, 64, 128, work=torch.float32).match(kda) == 0
     assert FuseKdaForward(1, 2, 1, 64, 128).match(
