@@ -81,14 +81,20 @@ def measured_traffic(kernel, lib_hash):
 
 def _counter_key(name, grid):
     """Record key of a dispatch in the counter passes: the headline's two kernels (the 32-column
-    scan and the 4096-chunk stage 1) and the KDA secondary's two; None for anything else (the
-    other secondaries, the calibration copies)."""
-    W = WORKLOAD
+    scan and the 4096-chunk stage 1), the long-context secondary's two (the 16-column scan and
+    the 16384-chunk stage 1) and the KDA secondary's two; None for anything else (the other
+    secondaries, the calibration copies)."""
+    W, L = WORKLOAD, LONG_WORKLOAD
     M = W["B"] * W["H"] * W["T"] // W["C"]
+    ML = L["B"] * L["H"] * L["T"] // L["C"]
     if "scan_split_kernel<64, 128, 128, 2," in name:
         return "scan_output"
+    if "scan_split_kernel<64, 128, 128, 1," in name:
+        return "long_scan_output"
     if "chunk_local_kernel" in name and "DF16b" in name and grid == M * 256:
         return "chunk_local"
+    if "chunk_local_kernel" in name and "DF16b" in name and grid == ML * 256:
+        return "long_chunk_local"
     for k in ("kda_scan", "kda_local"):
         if k in name:
             return k
@@ -125,9 +131,16 @@ def summarize_counters(fetch_db, write_db, lib_hash, copy_mib, out=None):
     model = stage_model(**{k: WORKLOAD[k] for k in ("B", "H", "T", "C", "DK", "DV")}, esize=2)
     kda = kda_model(**KDA_WORKLOAD)
     model_bytes = {k: model[k]["bytes"] for k in model if k in per}
+    lmodel = stage_model(**{k: LONG_WORKLOAD[k] for k in ("B", "H", "T", "C", "DK", "DV")},
+                         esize=2)
+    h0_bytes = LONG_WORKLOAD["B"] * LONG_WORKLOAD["H"] * LONG_WORKLOAD["DK"] * LONG_WORKLOAD["DV"] * 4
+    for k in ("chunk_local", "scan_output"):
+        if "long_" + k in per:
+            model_bytes["long_" + k] = lmodel[k]["bytes"] + (h0_bytes if k == "scan_output" else 0)
     model_bytes.update({k: kda[k] for k in ("kda_local", "kda_scan") if k in per})
-    rec = {"workload": "GDN forward B4 H16 T4096 C64 dk=dv=128, bf16 in (bench.py headline); KDA "
-                       "forward B2 H32 T8192 (bench.py kda_config5)",
+    rec = {"workload": "GDN forward B4 H16 T4096 C64 dk=dv=128, bf16 in (bench.py headline); "
+                       "long-context GDN B1 H32 T32768 with h0 (long_*: bench.py "
+                       "gdn_config4_long_context); KDA forward B2 H32 T8192 (bench.py kda_config5)",
            "source_hash": lib_hash,
            "commands": [f"rocprofv3 --pmc {c} -d <dir> -o <name> -- python bench.py --steps 3 "
                         f"--warmup 1 --no-cpu-baseline --event-steps 1 --calibrate-copy {copy_mib}"
@@ -203,6 +216,7 @@ def cpu_baseline(runs: int = 5, timeout: float = 600.0):
 
 
 KDA_WORKLOAD = dict(B=2, H=32, T=8192, C=64, DK=128, DV=128)
+LONG_WORKLOAD = dict(B=1, H=32, T=32768, C=64, DK=128, DV=128)
 
 
 def kda_model(B, H, T, C, DK, DV):
@@ -504,8 +518,9 @@ def main(argv=None) -> int:
         sec_steps, sec_warm = max(1, min(args.steps, 50)), min(max(args.warmup, 5), 10)
         line["secondary"] = {
             "kda_config5": kda_secondary(sec_steps, sec_warm),
-            "gdn_config4_long_context": gdn_config_secondary(1, 32, 32768, "bf16", 0.02, sec_steps,
-                                                             sec_warm),
+            "gdn_config4_long_context": gdn_config_secondary(
+                LONG_WORKLOAD["B"], LONG_WORKLOAD["H"], LONG_WORKLOAD["T"], "bf16", 0.02,
+                sec_steps, sec_warm),
             "kkt_inverse_config3": kkt_inverse_secondary(sec_steps, sec_warm),
             "deltanet_config1": gdn_config_secondary(1, 4, 512, "fp32", None, sec_steps,
                                                      sec_warm, kind="deltanet"),
