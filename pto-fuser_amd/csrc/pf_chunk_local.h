@@ -128,6 +128,11 @@ __device__ __forceinline__ void put16(float* M, int r, int cc, const floatx4& X,
 //      unused strictly-upper quadrant of As, then the four tiles of -T_R X.
 // The off-diagonal part is three levels of at most two dependent 16 x 16 products each (a
 // block-diagonal sweep would end in a chain of four).  Must be called by all 256 threads.
+//
+// Ts may equal As (in place): every block of T is written only after the last read of the A
+// block at its position — T_ii by wave 0 after it has read all of A_ii, T10 / T32 by the wave
+// that just read A10 / A32, and T_LL a barrier after the X products read A_LL — and X lives in
+// the strictly-upper quadrant, which neither A nor T occupies.
 __device__ __forceinline__ void unit_lower_inverse64(float* As, float* Ts) {
   constexpr int CP = 64 + 4;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
@@ -280,8 +285,8 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
   }
 }
 
-// One workgroup per chunk; four workgroups fit a CU (LDS), so the HBM latency of one chunk's
-// loads overlaps the other workgroups' products and inverse.
+// One workgroup per chunk; eight workgroups fit a CU for bf16 without P (four with P or fp32),
+// so the HBM latency of one chunk's loads overlaps the other workgroups' products and inverse.
 template <typename E, typename TO, int C, int DK, bool DO_P, bool DO_INV>
 __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   static_assert(C == 64, "the chunk-local kernel is written for 64-token chunks");
@@ -294,9 +299,10 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   constexpr int NVT = NV / 256;                     // per thread
   static_assert(NV % 256 == 0, "k/q chunk tile must divide over 256 threads");
   constexpr int KQ_BYTES = (DO_P ? 2 : 1) * C * KP * (int)sizeof(E);
-  constexpr int AT_BYTES = (DO_INV ? 2 : 1) * C * CP * 4;
-  // A and T are written only after the last score read of k/q (a barrier apart), so they reuse
-  // the k/q tiles' LDS: 35 KB per workgroup for bf16, four workgroups per CU.
+  constexpr int AT_BYTES = C * CP * 4;   // A, then T in its place
+  // A is written only after the last score read of k/q (a barrier apart), so it reuses the k/q
+  // tiles' LDS, and the inverse runs in place: 17.9 KB per workgroup for bf16 without P, eight
+  // workgroups per CU.
   constexpr int KQT_BYTES = KQ_BYTES > AT_BYTES ? KQ_BYTES : AT_BYTES;
 
   __shared__ __attribute__((aligned(16))) char kqt[KQT_BYTES];
@@ -305,7 +311,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
   E* ks = reinterpret_cast<E*>(kqt);
   E* qs = ks + C * KP;
   float* As = reinterpret_cast<float*>(kqt);
-  float* Ts = As + C * CP;
+  float* Ts = As;
 
   const int m = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -363,6 +369,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
       const int i = e / C, j = e % C;
       Ao[e] = (j < i) ? As[i * CP + j] : 0.f;
     }
+    lds_barrier();   // the inverse overwrites A in place
   }
 
   if (DO_INV) {

@@ -306,19 +306,19 @@ void scan_split_kernel(ScanOutArgs a) {
       const Stage& s = st[ch & 1];
       // ---- phase A: Y = k S~ and (q S~)^T for this wave's 16 tokens, r -> RX ----
       floatx4 Y[NT], QT[NT];
-      bf16x8 qf[DK / 32];                                 // q rows, kept for the score of phase B
+      bf16x8 kf[DK / 32], qf[DK / 32];                    // k, q rows, kept for the score
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) { Y[nt] = zero4(); QT[nt] = zero4(); }
 #pragma unroll
       for (int kb = 0; kb < DK / 32; ++kb) {
         const bf16* kp = s.ks + kq_rd + 32 * kb;
         const bf16* qp = s.qs + kq_rd + 32 * kb;
-        const bf16x8 ka = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
+        kf[kb] = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
         qf[kb] = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const bf16x8 sb = *reinterpret_cast<const bf16x8*>(SB + (kb * NT + nt) * FRAG + frag);
-          Y[nt] = mfma_bf16(ka, sb, Y[nt]);               // (k S~)[t][n]
+          Y[nt] = mfma_bf16(kf[kb], sb, Y[nt]);           // (k S~)[t][n]
           QT[nt] = mfma_bf16(sb, qf[kb], QT[nt]);         // (q S~)^T[n][t]
         }
       }
@@ -371,16 +371,18 @@ void scan_split_kernel(ScanOutArgs a) {
       // tiles are spread three, three, two, two over the waves so that each wave's phase carries
       // the same number of products; (2,0), (3,0) (wave 0) and (3,1) (wave 1) reach their owners
       // through PX after B2.
+      // A wave's own k and q rows (block cw) come from the registers of phase A, so every tile
+      // reads at most one operand block from LDS.
       bf16x4 ptl[4];                                     // this wave's own tiles (ib = cw)
       {
-        auto tile = [&](int ib, int jb) -> bf16x4 {
+        auto tile = [&](int ib, int jb, bool own_k, bool own_q) -> bf16x4 {
           floatx4 acc = zero4();
 #pragma unroll
           for (int kb = 0; kb < DK / 32; ++kb) {
             const bf16* kp = s.ks + kj_rd + 16 * jb * KP + 32 * kb;
             const bf16* qp = s.qs + kj_rd + 16 * ib * KP + 32 * kb;
-            const bf16x8 kr = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
-            const bf16x8 qr = ib == cw ? qf[kb] : cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+            const bf16x8 kr = own_k ? kf[kb] : cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
+            const bf16x8 qr = own_q ? qf[kb] : cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
             acc = mfma_bf16(kr, qr, acc);
           }
           const float gi = s.GT[16 * ib + c];
@@ -397,19 +399,19 @@ void scan_split_kernel(ScanOutArgs a) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) ptl[jb] = z4;
         if (cw == 0) {
-          ptl[0] = tile(0, 0);
-          *reinterpret_cast<bf16x4*>(PX + (0 * 64 + lane) * 4) = tile(2, 0);
-          *reinterpret_cast<bf16x4*>(PX + (1 * 64 + lane) * 4) = tile(3, 0);
+          ptl[0] = tile(0, 0, true, true);
+          *reinterpret_cast<bf16x4*>(PX + (0 * 64 + lane) * 4) = tile(2, 0, true, false);
+          *reinterpret_cast<bf16x4*>(PX + (1 * 64 + lane) * 4) = tile(3, 0, true, false);
         } else if (cw == 1) {
-          ptl[0] = tile(1, 0);
-          ptl[1] = tile(1, 1);
-          *reinterpret_cast<bf16x4*>(PX + (2 * 64 + lane) * 4) = tile(3, 1);
+          ptl[0] = tile(1, 0, false, true);
+          ptl[1] = tile(1, 1, true, true);
+          *reinterpret_cast<bf16x4*>(PX + (2 * 64 + lane) * 4) = tile(3, 1, true, false);
         } else if (cw == 2) {
-          ptl[1] = tile(2, 1);
-          ptl[2] = tile(2, 2);
+          ptl[1] = tile(2, 1, false, true);
+          ptl[2] = tile(2, 2, true, true);
         } else {
-          ptl[2] = tile(3, 2);
-          ptl[3] = tile(3, 3);
+          ptl[2] = tile(3, 2, false, true);
+          ptl[3] = tile(3, 3, true, true);
         }
       }
       lds_barrier();                                     // B2
