@@ -35,16 +35,18 @@
 // compute waves work on chunk c (three rotating register sets), and chunk c+1 written into the
 // free half of a double-buffered LDS stage (k and q rows swizzled for the permuted-K operand
 // reads and the transposed k^T reads, T rows, the v tile row-major, per-token gate tables).
-// Both are spread over the three phases of the interval (k and q loads and k's LDS rows in the
-// first, T in the second, v, the gates and q's rows in the third), and the loader waves run
-// at the default wave priority: a burst of loads or LDS writes issued at once, or at a raised
-// priority, was measured to stall the compute waves sharing the SIMDs (one phase lost up to
-// 1 000 cycles).  The compute waves store their o rows themselves, one 16-byte store per lane and
-// column block.  The loaders also carry the deferred state decay: the compute waves hold
+// Both are spread over the three phases of the interval (k's loads and LDS rows in the first,
+// T's and q's loads and T's rows in the second, v, the gates and q's rows in the third), and the
+// loader waves run at the default wave priority: a burst of loads or LDS writes issued at once,
+// or at a raised priority, was measured to stall the compute waves sharing the SIMDs (one phase
+// lost up to 1 000 cycles; q's loads in the first phase beside k's cost 5 % of the kernel).
+// The compute waves store their o rows themselves, one 16-byte store per lane and column block.  The loaders also carry the deferred state decay: the compute waves hold
 // S~ = S / f with a running factor f folded into the gate tables, and multiply it back only when
 // the loader flags a renormalisation (f below e^-60, or the last chunk, so the final state is
 // exact).
 #pragma once
+
+#include <type_traits>
 
 #include "pf_gfx950.h"
 
@@ -65,8 +67,18 @@ struct SplitStage {
   float BEG[C];   // beta_t e^{G_t} f_c
   float EGS[C];   // scale e^{G_t} f_c
   float EL[C];    // e^{G_last - G_t} / f_{c+1}
-  float DL[4];    // [0] factor for the state at this chunk's update, [1] nonzero: apply it
+  float CB[C];    // score gate, key side: e^{G_{16 (t / 16)} - G_t}
+  float RA[160];  // score gate, query side: scale e^{G_{16 ib + c} - G_{16 jb}}, [tile(ib, jb)][c]
+  float DL[4];    // [0] factor for the state at this chunk's update, [1] nonzero: apply it,
+                  // [2] nonzero: the score gates are evaluated per element (CB, RA not valid)
 };
+
+// Index of the lower-triangular 16x16 score tile (ib, jb), jb <= ib, in Stage::RA.
+__device__ __forceinline__ constexpr int score_tile_index(int ib, int jb) { return ib * (ib + 1) / 2 + jb; }
+
+// Decay inside one 16-token block (G at its start minus G at its end) up to which the factored
+// score gate e^{G_i - G_j} = e^{G_i - G_m} e^{G_m - G_j} is used: its key factor stays below e^80.
+constexpr float kScoreGateSpan = 80.f;
 
 // Loader register image of one chunk (k, q: 1024 16-byte vectors; T, P: 512; v: 8 NCOL).
 template <int NLW, int NCOL>
@@ -156,6 +168,13 @@ void scan_split_kernel(ScanOutArgs a) {
       for (int i = 0; i < Regs::NK; ++i) {
         const uint32_t rowi = krow_i(i);
         r.k[i] = buf_load16(rk, kq_voff, kq_s + rowi * DK * 2);
+      }
+    };
+    auto load_q = [&](Regs& r, int ch) {
+      const uint32_t kq_s = (uint32_t)ch * C * DK * 2;
+#pragma unroll
+      for (int i = 0; i < Regs::NK; ++i) {
+        const uint32_t rowi = krow_i(i);
         r.q[i] = buf_load16(rq, kq_voff, kq_s + rowi * DK * 2);
       }
     };
@@ -218,6 +237,39 @@ void scan_split_kernel(ScanOutArgs a) {
       Lrun = Lnext;
     };
 
+    // Score gate tables of a chunk.  P[i][j] = scale e^{min(G_i - G_j, 0)} (q_i . k_j) for
+    // j <= i; with G non-increasing through the chunk (every g <= 0) the clamp is inactive and,
+    // with m = 16 jb the first token of j's block, e^{G_i - G_j} = RA (<= scale: i >= m) * CB[j]
+    // (>= 1, at most e^kScoreGateSpan): two finite factors, and no exponential in the compute
+    // waves.  Any other chunk (a g > 0, a steeper block, a non-finite G) sets DL[2] and takes the
+    // per-element path.  Loader wave lw writes the RA column jb = lw (lanes = query tokens, G from
+    // its own lane and the block starts read as scalars); wave 0 also CB and the flag.
+    auto store_gates = [&](Stage& s, const Regs& r) {
+      const int t = lt & (C - 1), lw = lt >> 6;
+      float gb[4], ge[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        gb[b] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.g), 16 * b));
+        ge[b] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r.g), 16 * b + 15));
+      }
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+        if (jb % NLW == lw && t >= 16 * jb)
+          s.RA[score_tile_index(t >> 4, jb) * 16 + (t & 15)] = oscale * __expf(r.g - gb[jb]);
+      if (lw == 0) {
+        const float gblk = t < 16 ? gb[0] : t < 32 ? gb[1] : t < 48 ? gb[2] : gb[3];
+        s.CB[t] = __expf(gblk - r.g);
+        // G_{t-1} from the neighbouring lane (DPP wave shift right by one)
+        const float gprev = __int_as_float(__builtin_amdgcn_update_dpp(
+            __float_as_int(r.g), __float_as_int(r.g), 0x138, 0xf, 0xf, false));
+        bool ok = t == 0 || r.g <= gprev;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) ok = ok && gb[b] - ge[b] <= kScoreGateSpan;
+        const bool fact = __all(ok);
+        if (t == 0) s.DL[2] = fact ? 0.f : 1.f;
+      }
+    };
+
     // Interval j (the compute waves work on chunk j from stage j & 1): chunk j+3's loads go into
     // the register set that held chunk j, chunk j+1 (loaded two intervals earlier) into stage
     // (j+1) & 1.  Chunk m lives in register set m % 3; past the end the loads repeat the last
@@ -232,7 +284,9 @@ void scan_split_kernel(ScanOutArgs a) {
       store_k(sn, nx);
       lds_barrier();                                     // B1
       load_tp(ld, nl);
+      load_q(ld, nl);
       store_tp(sn, nx);
+      store_gates(sn, nx);
       lds_barrier();                                     // B2
       load_vg(ld, nl);
       store_vg(sn, nx, j + 1);
@@ -245,17 +299,21 @@ void scan_split_kernel(ScanOutArgs a) {
       lds_barrier();
     };
     load_kq(r0, 0);
+    load_q(r0, 0);
     load_tp(r0, 0);
     load_vg(r0, 0);
     load_kq(r1, min(1, last));
+    load_q(r1, min(1, last));
     load_tp(r1, min(1, last));
     load_vg(r1, min(1, last));
     load_kq(r2, min(2, last));
+    load_q(r2, min(2, last));
     load_tp(r2, min(2, last));
     load_vg(r2, min(2, last));
     store_k(st[0], r0);
     store_q(st[0], r0);
     store_tp(st[0], r0);
+    store_gates(st[0], r0);
     store_vg(st[0], r0, 0);
     lds_barrier();                                       // start: stage 0 and SB ready
     if (NC > 1) {
@@ -375,44 +433,62 @@ void scan_split_kernel(ScanOutArgs a) {
       // reads at most one operand block from LDS.
       bf16x4 ptl[4];                                     // this wave's own tiles (ib = cw)
       {
-        auto tile = [&](int ib, int jb, bool own_k, bool own_q) -> bf16x4 {
-          floatx4 acc = zero4();
+        // one straight-line copy of the score block per gate path (a branch inside each tile
+        // would keep the scheduler from overlapping one tile's gating with the next's products)
+        const bool gate_exact = __builtin_amdgcn_readfirstlane(__float_as_int(s.DL[2])) != 0;
+        auto score_tiles = [&](auto exact_tag) {
+          constexpr bool kExact = decltype(exact_tag)::value;
+          auto tile = [&](int ib, int jb, bool own_k, bool own_q) -> bf16x4 {
+            floatx4 acc = zero4();
 #pragma unroll
-          for (int kb = 0; kb < DK / 32; ++kb) {
-            const bf16* kp = s.ks + kj_rd + 16 * jb * KP + 32 * kb;
-            const bf16* qp = s.qs + kj_rd + 16 * ib * KP + 32 * kb;
-            const bf16x8 kr = own_k ? kf[kb] : cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
-            const bf16x8 qr = own_q ? qf[kb] : cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
-            acc = mfma_bf16(kr, qr, acc);
-          }
-          const float gi = s.GT[16 * ib + c];
-          const floatx4 gj = *reinterpret_cast<const floatx4*>(s.GT + 16 * jb + 4 * g);
-          bf16x4 out;
+            for (int kb = 0; kb < DK / 32; ++kb) {
+              const bf16* kp = s.ks + kj_rd + 16 * jb * KP + 32 * kb;
+              const bf16* qp = s.qs + kj_rd + 16 * ib * KP + 32 * kb;
+              const bf16x8 kr = own_k ? kf[kb] : cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
+              const bf16x8 qr = own_q ? qf[kb] : cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+              acc = mfma_bf16(kr, qr, acc);
+            }
+            bf16x4 out;
+            if constexpr (!kExact) {
+              const float ra = s.RA[score_tile_index(ib, jb) * 16 + c];
+              const floatx4 cb = *reinterpret_cast<const floatx4*>(s.CB + 16 * jb + 4 * g);
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const float keep = (jb < ib || c >= 4 * g + ii) ? oscale : 0.f;
-            out[ii] = (bf16)(keep * acc[ii] * __expf(fminf(gi - gj[ii], 0.f)));
+              for (int ii = 0; ii < 4; ++ii)
+                out[ii] = (bf16)((jb < ib || c >= 4 * g + ii) ? acc[ii] * (ra * cb[ii]) : 0.f);
+            } else {
+              const float gi = s.GT[16 * ib + c];
+              const floatx4 gj = *reinterpret_cast<const floatx4*>(s.GT + 16 * jb + 4 * g);
+#pragma unroll
+              for (int ii = 0; ii < 4; ++ii) {
+                const float keep = (jb < ib || c >= 4 * g + ii) ? oscale : 0.f;
+                out[ii] = (bf16)(keep * acc[ii] * __expf(fminf(gi - gj[ii], 0.f)));
+              }
+            }
+            return out;
+          };
+          if (cw == 0) {
+            ptl[0] = tile(0, 0, true, true);
+            *reinterpret_cast<bf16x4*>(PX + (0 * 64 + lane) * 4) = tile(2, 0, true, false);
+            *reinterpret_cast<bf16x4*>(PX + (1 * 64 + lane) * 4) = tile(3, 0, true, false);
+          } else if (cw == 1) {
+            ptl[0] = tile(1, 0, false, true);
+            ptl[1] = tile(1, 1, true, true);
+            *reinterpret_cast<bf16x4*>(PX + (2 * 64 + lane) * 4) = tile(3, 1, true, false);
+          } else if (cw == 2) {
+            ptl[1] = tile(2, 1, false, true);
+            ptl[2] = tile(2, 2, true, true);
+          } else {
+            ptl[2] = tile(3, 2, false, true);
+            ptl[3] = tile(3, 3, true, true);
           }
-          return out;
         };
         const bf16x4 z4 = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) ptl[jb] = z4;
-        if (cw == 0) {
-          ptl[0] = tile(0, 0, true, true);
-          *reinterpret_cast<bf16x4*>(PX + (0 * 64 + lane) * 4) = tile(2, 0, true, false);
-          *reinterpret_cast<bf16x4*>(PX + (1 * 64 + lane) * 4) = tile(3, 0, true, false);
-        } else if (cw == 1) {
-          ptl[0] = tile(1, 0, false, true);
-          ptl[1] = tile(1, 1, true, true);
-          *reinterpret_cast<bf16x4*>(PX + (2 * 64 + lane) * 4) = tile(3, 1, true, false);
-        } else if (cw == 2) {
-          ptl[1] = tile(2, 1, false, true);
-          ptl[2] = tile(2, 2, true, true);
-        } else {
-          ptl[2] = tile(3, 2, false, true);
-          ptl[3] = tile(3, 3, true, true);
-        }
+        if (gate_exact)
+          score_tiles(std::true_type{});
+        else
+          score_tiles(std::false_type{});
       }
       lds_barrier();                                     // B2
       // ---- phase C: o^T = v_new^T P^T + scale e^G f (q S~)^T -> HBM; S~ update -> SB ----

@@ -116,6 +116,40 @@ def test_gdn_bf16_short_sequences(B, H, T, h0):
     _check(f"GDN bf16 B{B} H{H} T{T}{' h0' if h0 else ''}", o, h, o_ref, h_ref, bf16=True)
 
 
+def _gate_case(name, T, seed):
+    """Per-token log decay g [1, 2, T] for the score-gate cases of the scan kernel."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(1, 2, T, generator=gen)
+    sp = torch.nn.functional.softplus
+    if name == "mixed_sign":          # g > 0 in places: the clamp of e^{min(G_i - G_j, 0)} acts
+        return x * 0.05 - 0.03
+    if name == "steep":               # > 80 of decay inside a 16-token block
+        return -sp(x) * 12.0
+    if name == "near_limit":          # about 70 per block: the factored gate's largest key factor
+        return -torch.full_like(x, 70.0 / 15)
+    if name == "alternating":         # steep and gentle chunks in one sequence
+        g = -sp(x) * 0.1
+        steep = (torch.arange(T) // 64) % 2 == 1
+        g[..., steep] = -sp(x[..., steep]) * 12.0
+        return g
+    raise ValueError(name)
+
+
+@pytest.mark.parametrize("name", ["mixed_sign", "steep", "near_limit", "alternating"])
+def test_gdn_bf16_score_gates(name):
+    """The scan forms the causal score's gate e^{min(G_i - G_j, 0)} from per-chunk factor tables
+    when G falls through the chunk and no 16-token block decays by more than 80, and per
+    element otherwise (a rising G, steeper blocks); both paths against the oracle."""
+    T = 1024
+    announce(f"GDN bf16 score gates {name} B1 H2 T{T}")
+    inp = make_delta_inputs(1, 2, T, kind="gdn", dtype=torch.bfloat16, seed=11, h0_std=0.02)
+    inp["g"] = _gate_case(name, T, 12).float()
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    assert np.isfinite(o).all() and np.isfinite(h).all()
+    _check(f"GDN bf16 score gates {name}", o, h, o_ref, h_ref, bf16=True)
+
+
 def test_gdn_bf16_config2():
     announce("GDN bf16 B4 H16 T4096")
     inp = make_delta_inputs(4, 16, 4096, kind="gdn", dtype=torch.bfloat16, seed=0)
