@@ -9,6 +9,9 @@ namespace pf {
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
+// Cache-policy operand of the raw buffer builtins for a non-temporal (streaming) access.
+constexpr int kCachePolicyNT = 2;
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }

@@ -425,7 +425,7 @@ void kda_scan_kernel(KdaScanArgs a) {
         const int row = orow_l + (64 * NLW / 8) * i;
         const floatx4 x = *reinterpret_cast<const floatx4*>(os + row * OP + 4 * oseg);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro, o_voff + (uint32_t)((64 * NLW / 8) * i * DV) * 4,
-                                               (uint32_t)ch * C * DV * 4, 0);
+                                               (uint32_t)ch * C * DV * 4, kCachePolicyNT);   // streamed
       }
     };
     // Same schedule as the GDN scan kernel: step j (between barriers j and j+1) issues the loads

@@ -297,7 +297,7 @@ void scan_output_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int t = 16 * mb + 4 * g + ii;
-        ocol[(size_t)t * DV] = s.EG[t] * QS[mb][ii] + O[ii];
+        __builtin_nontemporal_store(s.EG[t] * QS[mb][ii] + O[ii], ocol + (size_t)t * DV);   // streamed
       }
     }
     // S = e^{G_last} S + k^T (v_new e^{G_last - G})

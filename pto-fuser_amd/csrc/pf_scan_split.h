@@ -511,7 +511,9 @@ void scan_split_kernel(ScanOutArgs a) {
               OT[nt] = mfma_bf16(*reinterpret_cast<const bf16x8*>(VX + (kb * NT + nt) * FRAG + frag), pb, OT[nt]);
           }
         }
-        // lane (c, g) holds o[token tok0 + c][columns 16 nt + 4g .. +3]: one 16-byte store each
+        // lane (c, g) holds o[token tok0 + c][columns 16 nt + 4g .. +3]: one 16-byte store each,
+        // non-temporal (o is never read here; streaming it past L2 leaves the cache to the k, q
+        // and T lines the chain's other column slices read: 7 % of the kernel's time)
         const float egs = s.EGS[tok0 + c];
         const uint32_t ooff = (uint32_t)(((size_t)ch * C + tok0 + c) * DV + col0 + 4 * g) * 4;
 #pragma unroll
@@ -519,7 +521,8 @@ void scan_split_kernel(ScanOutArgs a) {
           floatx4 val;
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) val[ii] = fmaf(egs, QT[nt][ii], OT[nt][ii]);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, ooff + 64 * nt, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, ooff + 64 * nt, 0,
+                                                 kCachePolicyNT);
         }
       }
       if (s.DL[1] != 0.f) {
