@@ -63,24 +63,25 @@ def test_measured_traffic_keyed_to_the_source_hash(tmp_path, monkeypatch):
 
 def test_recorded_counters_match_the_byte_model():
     """The committed counter record (whatever build it belongs to) agrees with the algorithmic
-    bytes of its kernels to within 0.5 %: no kernel re-reads.  The long-context scan's reads
-    hold the same bar; its writes may run up to 4 % over, since its 16-column slices write each
-    o row as half of a 128-byte line and a line that L2 evicts between the two halves is written
-    twice."""
+    bytes of its kernels: reads to within 0.5 % (no kernel re-reads), and so do the writes of
+    every kernel but the scans.  The scans store o non-temporally, a 64-byte half of a 128-byte
+    line per instruction, and a line whose halves reach memory separately is counted twice: their
+    writes may run up to 15 % over o and the final state."""
     with open(bench.COUNTERS) as f:
         rec = json.load(f)
     m = bench.stage_model(4, 16, 4096, C, DK, DV, 2)
+    scans = {"scan_output": bench.WORKLOAD, "long_scan_output": bench.LONG_WORKLOAD}
     for k, kib in rec["kernels"].items():
         traffic = sum(kib[c] * rec["scale"][c] * 1024 for c in ("FETCH_SIZE", "WRITE_SIZE"))
-        if k == "long_scan_output":
-            L = bench.LONG_WORKLOAD
+        if k in scans:
+            L = scans[k]
             o_final = L["B"] * L["H"] * (L["T"] * L["DV"] + L["DK"] * L["DV"]) * 4
             writes = kib["WRITE_SIZE"] * rec["scale"]["WRITE_SIZE"] * 1024
             reads = traffic - writes
             assert abs(reads / (rec["model_bytes"][k] - o_final) - 1) < 5e-3, (k, reads)
-            assert 0 <= writes / o_final - 1 < 0.04, (k, writes)
-            continue
-        assert abs(traffic / rec["model_bytes"][k] - 1) < 5e-3, (k, traffic)
+            assert 0 <= writes / o_final - 1 < 0.15, (k, writes)
+        else:
+            assert abs(traffic / rec["model_bytes"][k] - 1) < 5e-3, (k, traffic)
         if k in m:
             assert rec["model_bytes"][k] == m[k]["bytes"], k
 
