@@ -113,11 +113,12 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
  * gated operands k e^G, k e^-G, q e^G, k e^{G_last - G} from g, inverts (I + A) and builds the WY
  * factors W, U and the score; stage 2 carries the state in registers with a per-channel decay.
  * Math: kda_reference (_kda_full.py:42-76) plus an initial state h0 and the final state.
- *   q, k [B,H,T,DK] bf16; v [B,H,T,DV] bf16; beta [B,H,T] fp32; g [B,H,T,DK] fp32 (per-token,
- *   per-channel log decay, summed within each chunk of C tokens by the kernel); h0 [B,H,DK,DV]
- *   fp32 or NULL; o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV] fp32 or NULL.
- *   Supported: dtype PF_DTYPE_BF16, C = 64 or 128 (run as 64-token chunks), DK = DV = 128,
- *   T % C == 0, T >= 128.
+ *   q, k [B,H,T,DK] and v [B,H,T,DV] of `dtype`; beta [B,H,T] fp32; g [B,H,T,DK] fp32
+ *   (per-token, per-channel log decay, summed within each chunk of C tokens by the kernel);
+ *   h0 [B,H,DK,DV] fp32 or NULL; o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV]
+ *   fp32 or NULL.  Supported: dtype PF_DTYPE_BF16 (bf16 MFMA, T >= 128) or PF_DTYPE_F32 (fp32
+ *   operands and fp32 MFMA throughout, T >= 64), C = 64 or 128 (run as 64-token chunks),
+ *   DK = DV = 128, T % C == 0.  The workspace holds the stage-1 images in the operand type.
  * ------------------------------------------------------------------------------------------ */
 size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
 void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype);

@@ -5,6 +5,7 @@
 
 #include "../../include/pto_fuser_hip.h"
 #include "pf_kda.h"
+#include "pf_kda_f32.h"
 #include "pf_status.h"
 #include "pf_workspace.h"
 
@@ -16,31 +17,33 @@ constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 using KdaWorkspace = pf::Workspace;
 
-// Byte layout of the KDA workspace, M = B*H*T/C chunks:
-//   [ W | U | QE | KR  (each M*C*128 bf16) | P (M*C*C bf16) | DEC (M*128 fp32) ]
+// Byte layout of the KDA workspace, M = B*H*T/C chunks, E the operand type (bf16 or fp32):
+//   [ W | U | QE | KR  (each M*C*128 E) | P (M*C*C E) | DEC (M*128 fp32) ]
 struct KdaLayout {
   size_t w_off, u_off, q_off, k_off, p_off, d_off, total;
-  KdaLayout(size_t M, int C, int D) {
-    const size_t tile = align256(M * C * D * sizeof(bf16));
+  KdaLayout(size_t M, int C, int D, int dtype) {
+    const size_t esize = dtype == PF_DTYPE_BF16 ? sizeof(bf16) : sizeof(float);
+    const size_t tile = align256(M * C * D * esize);
     w_off = 0;
     u_off = w_off + tile;
     q_off = u_off + tile;
     k_off = q_off + tile;
     p_off = k_off + tile;
-    d_off = p_off + align256(M * C * C * sizeof(bf16));
+    d_off = p_off + align256(M * C * C * esize);
     total = d_off + align256(M * D * sizeof(float));
   }
 };
 
-// bf16 operands, C = 64, dk = dv = 128, at least two chunks per chain (the scan kernel's loader
-// pipeline is written for NC >= 2).
+// bf16 operands with at least two chunks per chain (the bf16 scan kernel's loader pipeline is
+// written for NC >= 2), or fp32 operands (the fp32 kernels of pf_kda_f32.h); dk = dv = 128.
 // 64-token chunks in the kernels; a caller's chunk size of 128 runs them over T / 64 chunks (the
 // chunked forward's result does not depend on the chunk size), with T a multiple of 128.
 constexpr int kChunk = 64;
 
 bool kda_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
   return B > 0 && H > 0 && T > 0 && (C == 64 || C == 128) && DK == 128 && DV == 128 &&
-         T % C == 0 && T / kChunk >= 2 && dtype == PF_DTYPE_BF16;
+         T % C == 0 &&
+         ((dtype == PF_DTYPE_BF16 && T / kChunk >= 2) || dtype == PF_DTYPE_F32);
 }
 
 }  // namespace
@@ -49,7 +52,7 @@ extern "C" {
 
 size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype) {
   if (!kda_shape_ok(B, H, T, C, DK, DV, dtype)) return 0;
-  return KdaLayout((size_t)B * H * (T / kChunk), kChunk, DK).total;
+  return KdaLayout((size_t)B * H * (T / kChunk), kChunk, DK, dtype).total;
 }
 
 void* pf_kda_create(void) { return pf::workspace_create(); }
@@ -78,12 +81,43 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   if (!kda_shape_ok(B, H, T, C, DK, DV, dtype)) return PF_ERR_ARG;
   const KdaWorkspace* w = static_cast<const KdaWorkspace*>(ws);
   const size_t M = (size_t)B * H * (T / kChunk);
-  const KdaLayout lay(M, kChunk, DK);
+  const KdaLayout lay(M, kChunk, DK, dtype);
   if (!w || !w->base || w->bytes < lay.total) return PF_ERR_WORKSPACE;
   if (!q || !k || !v || !beta || !g || !o) return PF_ERR_ARG;
   constexpr int KC = 64, KD = 128;
   char* base = static_cast<char*>(w->base);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == PF_DTYPE_F32) {
+    pf::KdaLocalF32Args la{};
+    la.q = static_cast<const float*>(q);
+    la.k = static_cast<const float*>(k);
+    la.v = static_cast<const float*>(v);
+    la.g = g;
+    la.beta = beta;
+    la.scale = scale;
+    la.W = reinterpret_cast<float*>(base + lay.w_off);
+    la.U = reinterpret_cast<float*>(base + lay.u_off);
+    la.QE = reinterpret_cast<float*>(base + lay.q_off);
+    la.KR = reinterpret_cast<float*>(base + lay.k_off);
+    la.P = reinterpret_cast<float*>(base + lay.p_off);
+    la.DEC = reinterpret_cast<float*>(base + lay.d_off);
+    pf::LaunchScope scope;
+    pf::kda_local_f32_kernel<KC, KD><<<dim3((unsigned)M), dim3(256), 0, s>>>(la);
+    pf::KdaScanF32Args sa{};
+    sa.W = la.W;
+    sa.U = la.U;
+    sa.QE = la.QE;
+    sa.KR = la.KR;
+    sa.P = la.P;
+    sa.DEC = la.DEC;
+    sa.h0 = h0;
+    sa.o = o;
+    sa.h_final = h_final;
+    sa.BH = B * H;
+    sa.NC = T / kChunk;
+    pf::kda_scan_f32_kernel<KC, KD, KD><<<dim3((unsigned)(B * H * (KD / 32))), dim3(128), 0, s>>>(sa);
+    return scope.status();
+  }
 
   pf::KdaLocalArgs la{};
   la.q = static_cast<const bf16*>(q);

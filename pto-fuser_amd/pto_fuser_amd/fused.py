@@ -322,15 +322,15 @@ def _gdn_forward_launch(inputs, params) -> List[torch.Tensor]:
 
 
 def _kda_forward_launch(inputs, params) -> List[torch.Tensor]:
-    """o [B,H,nc,C,D] fp32 = the KDA forward of qF, kF, vF [M,C,D] (bf16) with the per-channel
-    cumulative gate g_native [M,C,D] and beta_native [M,C] (_kda_full.py:42-160), through
-    pf_kda_exec."""
+    """o [B,H,nc,C,D] fp32 = the KDA forward of qF, kF, vF [M,C,D] (bf16, or fp32 end to end)
+    with the per-channel cumulative gate g_native [M,C,D] and beta_native [M,C]
+    (_kda_full.py:42-160), through pf_kda_exec."""
     q, k, v, g_native, beta_native = inputs
     B, H, nc, C, D = _whole_dims(q, params)
     T = nc * C
-    bf = torch.bfloat16
-    o, _ = ops.kda_chunk_forward(_op(q, bf, (B, H, T, D)), _op(k, bf, (B, H, T, D)),
-                                 _op(v, bf, (B, H, T, D)), _f32(beta_native, (B, H, T)),
+    dt = _operand_dtype(q, k, v)
+    o, _ = ops.kda_chunk_forward(_op(q, dt, (B, H, T, D)), _op(k, dt, (B, H, T, D)),
+                                 _op(v, dt, (B, H, T, D)), _f32(beta_native, (B, H, T)),
                                  _per_token_gate(g_native.reshape(-1, C, D)).reshape(B, H, T, D),
                                  scale=float(params["scale"]), chunk_size=C,
                                  output_final_state=False)
@@ -440,9 +440,9 @@ def default_fused_registry() -> FusedKernelRegistry:
         FusedContract(
             in_slots=["q", "k", "v", "g_native", "beta_native"],
             in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
-            notes="whole KDA forward: q/k/v [M,C,D] bf16, per-channel cumulative gate "
-                  "g_native [M,C,D] and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; C = 64 or "
-                  "128, D = 128, T >= 128")))
+            notes="whole KDA forward: q/k/v [M,C,D] (bf16, or fp32 end to end), per-channel "
+                  "cumulative gate g_native [M,C,D] and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; "
+                  "C = 64 or 128, D = 128, bf16 T >= 128")))
     return reg
 
 

@@ -368,12 +368,11 @@ def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
                       ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Fused chunked KDA forward (per-channel decay) on the current HIP stream.
 
-    q, k [B,H,T,DK] and v [B,H,T,DV] bfloat16; beta [B,H,T] float32; g [B,H,T,DK] float32 (the
-    per-token, per-channel log decay, summed within chunks by the kernel); h0 [B,H,DK,DV]
-    float32 or None.  Returns (o [B,H,T,DV] float32 scaled by ``scale`` (default DK^-1/2),
-    h_final [B,H,DK,DV] float32 or None).  chunk_size 64 or 128 (both run 64-token chunks); at
-    least two of them per sequence (T >= 128); float32 operands are served by the staged KDA
-    program (forwards.kda) instead."""
+    q, k [B,H,T,DK] and v [B,H,T,DV] bfloat16 or float32 (one dtype); beta [B,H,T] float32;
+    g [B,H,T,DK] float32 (the per-token, per-channel log decay, summed within chunks by the
+    kernel); h0 [B,H,DK,DV] float32 or None.  Returns (o [B,H,T,DV] float32 scaled by ``scale``
+    (default DK^-1/2), h_final [B,H,DK,DV] float32 or None).  chunk_size 64 or 128 (both run
+    64-token chunks); bfloat16 needs at least two 64-token chunks per sequence (T >= 128)."""
     if q.dim() != 4:
         raise ValueError(f"q must be [B,H,T,DK], got shape {tuple(q.shape)}")
     B, H, T, DK = q.shape
@@ -382,11 +381,12 @@ def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
     if C not in SUPPORTED_C or DK not in SUPPORTED_D or DV not in SUPPORTED_D:
         raise ValueError(f"unsupported shape C={C} DK={DK} DV={DV} "
                          f"(C in {SUPPORTED_C}, DK/DV in {SUPPORTED_D})")
-    if T % C or T // 64 < 2:
-        raise ValueError(f"T={T} must be a multiple of the chunk size {C} and hold at least two "
-                         f"chunks of 64 tokens")
-    if q.dtype != torch.bfloat16:
-        raise ValueError(f"the fused KDA forward takes bfloat16 operands, got {q.dtype}")
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"the fused KDA forward takes bfloat16 or float32 operands, got {q.dtype}")
+    if T % C:
+        raise ValueError(f"T={T} must be a multiple of the chunk size {C}")
+    if q.dtype == torch.bfloat16 and T // 64 < 2:
+        raise ValueError(f"T={T}: bfloat16 operands need at least two chunks of 64 tokens")
     dev = q.device
     if dev.type != "cuda":
         raise ValueError(f"q must be on a HIP device, got {dev}")
@@ -410,6 +410,6 @@ def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
     lib = _hip.load()
     st = lib.pf_kda_exec(_hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(beta), _hip.ptr(g),
                          _hip.ptr(h0), _hip.ptr(o), _hip.ptr(hf), B, H, T, C, DK, DV,
-                         _hip.PF_DTYPE_BF16, sc, ws.handle, _hip.current_stream_handle(dev))
+                         _dtype_code(q.dtype), sc, ws.handle, _hip.current_stream_handle(dev))
     _hip.check("pf_kda_exec", st)
     return o, hf

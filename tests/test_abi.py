@@ -81,13 +81,22 @@ def test_kda_workspace_and_rejects(lib):
     want = 4 * ((M * 64 * 128 * 2 + 255) // 256 * 256) + (M * 64 * 64 * 2 + 255) // 256 * 256 \
         + (M * 128 * 4 + 255) // 256 * 256
     assert lib.pf_kda_workspace_bytes(2, 32, 8192, 64, 128, 128, _hip.PF_DTYPE_BF16) == want
-    assert lib.pf_kda_workspace_bytes(1, 1, 8192, 64, 128, 128, _hip.PF_DTYPE_F32) == 0   # bf16 only
-    assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_BF16) == 0    # one chunk
+    # fp32 operands: the same images in fp32
+    M1 = 128
+    want32 = 4 * ((M1 * 64 * 128 * 4 + 255) // 256 * 256) + (M1 * 64 * 64 * 4 + 255) // 256 * 256 \
+        + (M1 * 128 * 4 + 255) // 256 * 256
+    assert lib.pf_kda_workspace_bytes(1, 1, 8192, 64, 128, 128, _hip.PF_DTYPE_F32) == want32
+    assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_F32) > 0     # one chunk
+    assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_BF16) == 0    # bf16: two
     assert not lib.pf_kda_setup(1, 1, 100, 64, 128, 128, 1)
     assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
                            1, 0.1, None, None) == _hip.PF_ERR_WORKSPACE
     assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
-                           0, 0.1, None, None) == _hip.PF_ERR_ARG
+                           0, 0.1, None, None) == _hip.PF_ERR_WORKSPACE                  # fp32 shape ok
+    assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
+                           7, 0.1, None, None) == _hip.PF_ERR_ARG                        # no such dtype
+    assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 64, 64, 128, 128,
+                           1, 0.1, None, None) == _hip.PF_ERR_ARG                        # bf16, one chunk
 
 
 def test_exec_rejects_contract_violations_before_launch(lib):
@@ -158,7 +167,7 @@ def test_ops_validate_on_host():
     gk = torch.zeros(1, 1, 128, 128)
     with pytest.raises(ValueError, match="HIP device"):
         kda_chunk_forward(qb, qb, qb, torch.zeros(1, 1, 128), gk)
-    with pytest.raises(ValueError, match="bfloat16"):
-        kda_chunk_forward(qb.float(), qb.float(), qb.float(), torch.zeros(1, 1, 128), gk)
+    with pytest.raises(ValueError, match="bfloat16 or float32"):
+        kda_chunk_forward(qb.half(), qb.half(), qb.half(), torch.zeros(1, 1, 128), gk)
     with pytest.raises(ValueError, match="two chunks"):
         kda_chunk_forward(qb[:, :, :64], qb[:, :, :64], qb[:, :, :64], torch.zeros(1, 1, 64), gk[:, :, :64])

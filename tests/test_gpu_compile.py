@@ -212,6 +212,31 @@ def test_whole_gdn_forward_fp32_program():
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-4
 
 
+def test_whole_kda_forward_fp32_program():
+    """fp32 work dtype: the whole KDA node runs the fused fp32 kernels (1e-4 relative), one
+    chunk per sequence included."""
+    for B, H, nc in ((1, 2, 3), (1, 3, 1)):
+        C, D = 64, 128
+        announce(f"whole-forward program kda fp32 B{B} H{H} nc{nc}")
+        inp = make_kda_inputs(B, H, nc, C, D, device=DEV, seed=23 + nc, dtype=torch.float32)
+        binds = prepare_kda_bindings(inp["q"], inp["k"], inp["v"], inp["beta"], inp["g_in"],
+                                     work=torch.float32)
+        T = nc * C
+        x = {n: t.double().cpu().numpy() for n, t in inp.items()}
+        ref, _ = kda_reference(x["q"].reshape(B, H, T, D), x["k"].reshape(B, H, T, D),
+                               x["v"].reshape(B, H, T, D), x["beta"].reshape(B, H, T),
+                               x["g_in"].reshape(B, H, T, D), C=C, dtype=np.float64)
+        prog = build_kda_program(B, H, nc, C, D, D ** -0.5, work=torch.float32)
+        whole = compile_program(prog, Features(B, H, nc, C, D, dtype=torch.float32,
+                                               per_dim_gate=True),
+                                policy=Policy(whole_forward=True), verify=False).program
+        assert [n.kernel for n in whole.nodes if isinstance(n, FusedNode)] == ["kda_forward"]
+        o = StagedExecutor().run(whole, binds)["o"]
+        torch.cuda.synchronize()
+        got = o.double().cpu().numpy().reshape(B, H, T, D)
+        assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-4
+
+
 @pytest.mark.parametrize("family", ["gdn", "kda"])
 def test_compile_program_keeps_whole_forward_verified(family):
     """With bindings the driver captures the whole-forward candidate into a HIP graph, gates it

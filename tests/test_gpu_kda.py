@@ -3,7 +3,7 @@
 kda_reference (oracle/gdn_oracle.py, restating examples/attention/_kda_full.py:42-76) consumes
 the bf16-rounded inputs upcast to float; the fused path computes in fp32 with bf16 MFMA operands.
 Tolerance, as for the other bf16 forwards: max abs err <= 2e-2 against the fp32 oracle on o AND
-the final state h.  Config 5 is the benchmark configuration B2 H32 T8192 with
+the final state h; fp32 operands (fp32 MFMA throughout) max rel err <= 1e-4.  Config 5 is the benchmark configuration B2 H32 T8192 with
 g = -softplus(N) * 0.05 per channel.
 """
 import numpy as np
@@ -18,6 +18,7 @@ from pto_fuser_amd.forwards import as_oracle_inputs, make_delta_inputs
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 BF16_TOL = 2e-2
+FP32_TOL = 1e-4
 
 
 def _run(inp):
@@ -31,6 +32,13 @@ def _check(case, o, h, o_ref, h_ref):
     for name, got, ref in (("o", o, o_ref), ("h", h, h_ref)):
         e = record_error(case, name, got, ref, f"max abs <= {BF16_TOL}")
         assert e["abs"] <= BF16_TOL, (case, name, e)
+
+
+def _check_fp32(case, o, h, o_ref, h_ref):
+    """fp32 operands: max rel err <= 1e-4 (relative to the reference's largest magnitude)."""
+    for name, got, ref in (("o", o, o_ref), ("h", h, h_ref)):
+        e = record_error(case, name, got, ref, f"max rel <= {FP32_TOL}")
+        assert e["rel"] <= FP32_TOL, (case, name, e)
 
 
 def _oracle(inp, dtype=np.float64):
@@ -104,3 +112,33 @@ def test_kda_linear_in_v_config5():
     o2, h2 = _run(dict(inp, v=inp["v"] * 2))
     assert np.array_equal(o2, 2 * o1), max_abs(o2, 2 * o1)
     assert np.array_equal(h2, 2 * h1), max_abs(h2, 2 * h1)
+
+
+@pytest.mark.parametrize("B,H,T,h0", [(1, 2, 64, False), (2, 3, 256, True), (1, 2, 512, True)])
+def test_kda_fp32_matches_oracle(B, H, T, h0):
+    """fp32 operands through the fp32 kernels (one chunk per sequence included)."""
+    announce(f"KDA fp32 B{B} H{H} T{T} h0={h0}")
+    inp = make_delta_inputs(B, H, T, kind="kda", dtype=torch.float32, seed=B * 13 + H * 5 + T,
+                            h0_std=0.02 if h0 else None)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    _check_fp32(f"KDA fp32 B{B} H{H} T{T}{' h0' if h0 else ''}", o, h, o_ref, h_ref)
+
+
+def test_kda_fp32_strong_decay_and_chunk_128():
+    """fp32 with faster decay, at C = 128 (run as 64-token chunks: the same result as C = 64,
+    bit for bit, and within the fp32 bound of the oracle chunked at 128)."""
+    announce("KDA fp32 B1 H2 T512 strong decay C128")
+    inp = make_delta_inputs(1, 2, 512, kind="kda", dtype=torch.float32, seed=17, gate_scale=0.3,
+                            h0_std=0.02)
+    d = {n: (None if t is None else t.to(DEV)) for n, t in inp.items()}
+    o128, h128 = kda_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"],
+                                   chunk_size=128)
+    o64, h64 = kda_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"])
+    torch.cuda.synchronize()
+    x = as_oracle_inputs(inp)
+    o_ref, h_ref = kda_reference(x["q"], x["k"], x["v"], x["beta"], x["g"], C=128, h0=x["h0"],
+                                 dtype=np.float64)
+    _check_fp32("KDA fp32 B1 H2 T512 strong decay C128", o128.cpu().numpy(), h128.cpu().numpy(),
+                o_ref, h_ref)
+    assert torch.equal(o128, o64) and torch.equal(h128, h64)
