@@ -13,8 +13,12 @@
 #include "pf_workspace.h"
 #include "pf_scan_output.h"
 #include "pf_scan_split.h"
+#include "pf_scan_split_f32.h"
 
 // loader waves of the split scan kernel for 32-column and for 16-column slices
+#ifndef PF_F32_SPLIT
+#define PF_F32_SPLIT 2
+#endif
 #ifndef PF_SPLIT_LW
 #define PF_SPLIT_LW 4
 #endif
@@ -131,6 +135,9 @@ void scan_output_launch(const void* q, const void* k, const void* v, const float
     else
       pf::scan_split_kernel<C, DK, DV, 2, PF_SPLIT_LW>
           <<<dim3((unsigned)(BH * (DV / 32))), dim3(64 * (4 + PF_SPLIT_LW)), 0, stream>>>(a);
+  } else if (PF_F32_SPLIT == 1 || (PF_F32_SPLIT == 2 && (size_t)BH * (DV / 16) <= (size_t)device_cu_count())) {
+    // fp32, few chains: every chunk split over four waves (pf_scan_split_f32.h)
+    pf::scan_split_f32_kernel<C, DK, DV><<<dim3((unsigned)(BH * (DV / 16))), dim3(256), 0, stream>>>(a);
   } else {
     // fp32: transposed tiles staged by the loader; one LDS buffer (the images are 143 KB)
     const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));

@@ -1,0 +1,206 @@
+// Stage 2 for fp32 operands with every chunk's work split over four waves: the state scan fused
+// with the output, for short sequences and few chains, where one wave walking a chain's whole
+// chunk (pf_scan_output.h) leaves the chain's latency as the forward's time.
+//
+// Workgroup = one chain bh x one 16-column slice (grid BH * DV / 16), four waves.  Wave w owns
+// state rows 32w .. 32w+31 (fp32, MFMA D layout, in registers for the whole chain).  Per chunk
+// (T, P, G from stage 1; fp32 MFMA 16x16x4 throughout):
+//
+//   1. partial Y_w = k[:, rows of w] S_w and (q S)_w for all 64 tokens     -> LDS
+//   2. every wave: Y = sum of the partials, r = beta v - beta e^G Y, v_new = T r (all tokens);
+//      wave w: o for tokens 16w .. 16w+15 = scale e^G (sum of the q S partials) + P v_new -> HBM;
+//      S_w <- e^{G_last} S_w + k[:, rows of w]^T (e^{G_last - G} v_new)
+//
+// so the chain carries 64 + 40 + 32 products per wave per chunk instead of one wave's ~460.  The
+// next chunk's k, q, T, P, v and gates are loaded into registers while a chunk is computed and
+// written into the (single) LDS image between two barriers.
+#pragma once
+
+#include "pf_scan_output.h"
+
+namespace pf {
+
+template <int C, int DK, int DV>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void scan_split_f32_kernel(ScanOutArgs a) {
+  static_assert(C == 64 && DK == 128 && DV % 16 == 0, "tile shapes of the fp32 split scan: C 64, DK 128");
+  constexpr int KP = DK + 4, TP = C + 4, VP = 16 + 4;
+  constexpr int NK = C * DK / 4 / 256, NT = C * C / 4 / 256;   // float4 copies per thread
+  __shared__ __attribute__((aligned(16))) float ks[C * KP];
+  __shared__ __attribute__((aligned(16))) float qs[C * KP];
+  __shared__ __attribute__((aligned(16))) float ts[C * TP];
+  __shared__ __attribute__((aligned(16))) float ps[C * TP];
+  __shared__ __attribute__((aligned(16))) float vs[C * VP];
+  __shared__ __attribute__((aligned(16))) float Bs[C], BEG[C], EG[C], EL[C], DL[4];
+  __shared__ __attribute__((aligned(16))) floatx4 YP[4 * 4 * 64];   // [wave][token tile][lane]
+  __shared__ __attribute__((aligned(16))) floatx4 QP[4 * 4 * 64];
+
+  constexpr int NS = DV / 16;
+  const int bh = blockIdx.x / NS, col0 = 16 * (blockIdx.x % NS);
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int NC = a.NC;
+  const size_t Tlen = (size_t)NC * C;
+  const float* kb = static_cast<const float*>(a.k) + (size_t)bh * Tlen * DK;
+  const float* qb = static_cast<const float*>(a.q) + (size_t)bh * Tlen * DK;
+  const float* vb = static_cast<const float*>(a.v) + (size_t)bh * Tlen * DV;
+  const float* tb = static_cast<const float*>(a.Tm) + (size_t)bh * NC * C * C;
+  const float* pb = static_cast<const float*>(a.P) + (size_t)bh * NC * C * C;
+  const float oscale = *a.scale;
+
+  // ---- one chunk: global -> registers -> LDS ----
+  floatx4 rk[NK], rq[NK], rt[NT], rp[NT], rv;
+  float rg = 0.f, rb = 0.f;
+  auto load = [&](int ch) {
+    const size_t t0 = (size_t)ch * C;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
+      rk[i] = *reinterpret_cast<const floatx4*>(kb + (t0 + row) * DK + 4 * q4);
+      rq[i] = *reinterpret_cast<const floatx4*>(qb + (t0 + row) * DK + 4 * q4);
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const int u = tid + 256 * i, row = u >> 4, q4 = u & 15;
+      rt[i] = *reinterpret_cast<const floatx4*>(tb + ((size_t)ch * C + row) * C + 4 * q4);
+      rp[i] = *reinterpret_cast<const floatx4*>(pb + ((size_t)ch * C + row) * C + 4 * q4);
+    }
+    rv = *reinterpret_cast<const floatx4*>(vb + (t0 + (tid >> 2)) * DV + col0 + 4 * (tid & 3));
+    if (tid < C) {
+      rg = a.G ? a.G[(size_t)bh * Tlen + t0 + tid] : 0.f;
+      rb = a.beta[(size_t)bh * Tlen + t0 + tid];
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
+      *reinterpret_cast<floatx4*>(ks + row * KP + 4 * q4) = rk[i];
+      *reinterpret_cast<floatx4*>(qs + row * KP + 4 * q4) = rq[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const int u = tid + 256 * i, row = u >> 4, q4 = u & 15;
+      *reinterpret_cast<floatx4*>(ts + row * TP + 4 * q4) = rt[i];
+      *reinterpret_cast<floatx4*>(ps + row * TP + 4 * q4) = rp[i];
+    }
+    *reinterpret_cast<floatx4*>(vs + (tid >> 2) * VP + 4 * (tid & 3)) = rv;
+    if (w == 0) {                                     // lane = token
+      const float gl = __shfl(rg, C - 1);
+      Bs[lane] = rb;
+      BEG[lane] = rb * __expf(rg);
+      EG[lane] = oscale * __expf(rg);
+      EL[lane] = __expf(gl - rg);
+      if (lane == 0) DL[0] = __expf(gl);
+    }
+  };
+
+  floatx4 S[2];                                       // rows 32w + 16r + 4g + ii, column col0 + c
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii)
+      S[r][ii] = a.h0 ? a.h0[((size_t)bh * DK + 32 * w + 16 * r + 4 * g + ii) * DV + col0 + c] : 0.f;
+
+  load(0);
+  store();
+  lds_barrier();
+  if (NC > 1) load(1);
+
+  for (int ch = 0; ch < NC; ++ch) {
+    // ---- 1. partial products over this wave's 32 state rows ----
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      floatx4 y = zero4(), qy = zero4();
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const floatx4 ka = *reinterpret_cast<const floatx4*>(ks + (16 * ib + c) * KP + 32 * w + 16 * r + 4 * g);
+        const floatx4 qa = *reinterpret_cast<const floatx4*>(qs + (16 * ib + c) * KP + 32 * w + 16 * r + 4 * g);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          y = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[ii], S[r][ii], y, 0, 0, 0);
+          qy = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[ii], S[r][ii], qy, 0, 0, 0);
+        }
+      }
+      YP[(w * 4 + ib) * 64 + lane] = y;
+      QP[(w * 4 + ib) * 64 + lane] = qy;
+    }
+    lds_barrier();
+    // ---- 2. r, v_new = T r for all tokens; o for tokens 16w ..; the update of rows 32w .. ----
+    floatx4 VN[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      floatx4 Y = YP[ib * 64 + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < 4; ++w2) Y += YP[(w2 * 4 + ib) * 64 + lane];
+      floatx4 R;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int t = 16 * ib + 4 * g + ii;
+        R[ii] = Bs[t] * vs[t * VP + c] - BEG[t] * Y[ii];
+      }
+      VN[ib] = R;                                      // r until the T products below
+    }
+    {
+      floatx4 V[4];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        floatx4 acc = zero4();
+#pragma unroll
+        for (int jb = 0; jb <= ib; ++jb) {
+          const floatx4 ta = *reinterpret_cast<const floatx4*>(ts + (16 * ib + c) * TP + 16 * jb + 4 * g);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[ii], VN[jb][ii], acc, 0, 0, 0);
+        }
+        V[ib] = acc;
+      }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) VN[ib] = V[ib];
+    }
+    {
+      floatx4 O = QP[w * 64 + lane];
+#pragma unroll
+      for (int w2 = 1; w2 < 4; ++w2) O += QP[(w2 * 4 + w) * 64 + lane];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[16 * w + 4 * g + ii];
+      for (int jb = 0; jb <= w; ++jb) {
+        const floatx4 pa = *reinterpret_cast<const floatx4*>(ps + (16 * w + c) * TP + 16 * jb + 4 * g);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) O = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ii], VN[jb][ii], O, 0, 0, 0);
+      }
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        __builtin_nontemporal_store(O[ii], a.o + ((size_t)bh * Tlen + (size_t)ch * C + 16 * w + 4 * g + ii) * DV + col0 + c);
+    }
+    {
+      const float dl = DL[0];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        floatx4 acc = S[r] * dl;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int t = 16 * jb + 4 * g + ii;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[t * KP + 32 * w + 16 * r + c], EL[t] * VN[jb][ii], acc, 0, 0, 0);
+          }
+        S[r] = acc;
+      }
+    }
+    lds_barrier();                                     // the chunk's image and partials are read
+    if (ch + 1 < NC) {
+      store();
+      lds_barrier();
+      if (ch + 2 < NC) load(ch + 2);
+    }
+  }
+  if (a.h_final) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        a.h_final[((size_t)bh * DK + 32 * w + 16 * r + 4 * g + ii) * DV + col0 + c] = S[r][ii];
+  }
+}
+
+}  // namespace pf
