@@ -116,12 +116,24 @@ __device__ __forceinline__ void put16(float* M, int r, int cc, const floatx4& X,
   for (int ii = 0; ii < 4; ++ii) M[(r + 4 * g + ii) * CP + cc + c] = sign * X[ii];
 }
 
+// x of lane p of this lane's quad (DPP quad_perm broadcast; p folds to a constant where the
+// caller's loop is unrolled).
+template <int P>
+__device__ __forceinline__ float quad_broadcast_c(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), P * 0x55, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float quad_broadcast(float x, int p) {
+  switch (p) {
+    case 0: return quad_broadcast_c<0>(x);
+    case 1: return quad_broadcast_c<1>(x);
+    case 2: return quad_broadcast_c<2>(x);
+    default: return quad_broadcast_c<3>(x);
+  }
+}
+
 // (I + A)^-1 of one strictly-lower 64 x 64 block (As, fp32, pitch 68) into Ts, by 16-row blocks:
-//   1. the four diagonal blocks by forward substitution in one wave, one lane per (block,
-//      column); each row's dot product runs over four accumulators, and the strictly-lower
-//      rows are read as broadcast vectors in batches, each issued before the previous batch's
-//      rows are consumed, so the LDS latency is paid about once per batch instead of once per
-//      row;
+//   1. the four diagonal blocks by right-looking forward substitution, one wave per block, four
+//      lanes per column (each holding four rows of it and those rows of A in registers);
 //   2. T10 = -T11 A10 T00 and T32 = -T33 A32 T22 (two waves);
 //   3. the lower-left 32 x 32 quadrant T_LL = -T_R (A_LL T_L), T_L / T_R the inverted upper-left
 //      / lower-right quadrants: the four 16 x 16 tiles of X = A_LL T_L (one per wave) go to the
@@ -130,56 +142,36 @@ __device__ __forceinline__ void put16(float* M, int r, int cc, const floatx4& X,
 // block-diagonal sweep would end in a chain of four).  Must be called by all 256 threads.
 //
 // Ts may equal As (in place): every block of T is written only after the last read of the A
-// block at its position — T_ii by wave 0 after it has read all of A_ii, T10 / T32 by the wave
+// block at its position — T_ii by the wave that has read all of A_ii, T10 / T32 by the wave
 // that just read A10 / A32, and T_LL a barrier after the X products read A_LL — and X lives in
 // the strictly-upper quadrant, which neither A nor T occupies.
 __device__ __forceinline__ void unit_lower_inverse64(float* As, float* Ts) {
   constexpr int CP = 64 + 4;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (w == 0) {
-    const int r = lane >> 4, cc = lane & 15;
+  {  // wave w inverts diagonal block w: lane = column cc (of T) x row phase p (rows 4k + p)
+    const int r = w, cc = lane >> 2, p = lane & 3;
     const float* Ab = As + (16 * r) * CP + 16 * r;
-    // row i holds columns 0 .. i-1: ceil(i / 4) vectors; five batches of at most eight vectors
-    // (rows 1-6, 7-9, 10-11, 12-13, 14-15), two in registers at a time
-    auto row0 = [](int bt) constexpr {
-      return bt == 0 ? 1 : bt == 1 ? 7 : bt == 2 ? 10 : bt == 3 ? 12 : bt == 4 ? 14 : 16;
-    };
-    floatx4 buf[2][8];
-    auto load_batch = [&](floatx4* dst, int bt) __attribute__((always_inline)) {
-      int n = 0;
+    // this lane's rows of A_rr, columns 0 .. 4k+3 (A is zero on and above the diagonal)
+    floatx4 arow[4][4];
 #pragma unroll
-      for (int i = row0(bt); i < row0(bt + 1); ++i)
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int q = 0; q < (i + 3) / 4; ++q)
-          dst[n++] = *reinterpret_cast<const floatx4*>(Ab + i * CP + 4 * q);
-    };
-    float t[16];
+      for (int q = 0; q <= k; ++q) arow[k][q] = *reinterpret_cast<const floatx4*>(Ab + (4 * k + p) * CP + 4 * q);
+    float s[4];                                        // rows 4k + p of column cc of T_rr
 #pragma unroll
-    for (int i = 0; i < 16; ++i) t[i] = (i == cc) ? 1.f : 0.f;
-    load_batch(buf[0], 0);
+    for (int k = 0; k < 4; ++k) s[k] = (4 * k + p == cc) ? 1.f : 0.f;
+    // right-looking substitution: once row j of the column is final, subtract its share from
+    // every later row; row j comes from lane (cc, j & 3) of the quad (a DPP broadcast), so the
+    // dependent chain is one broadcast and one fused multiply-add per row
 #pragma unroll
-    for (int bt = 0; bt < 5; ++bt) {
-      if (bt < 4) load_batch(buf[(bt + 1) & 1], bt + 1);
-      __builtin_amdgcn_sched_barrier(0);   // keep the batch's reads ahead of this batch's math
-      const floatx4* rows = buf[bt & 1];
-      int n = 0;
+    for (int j = 0; j < 15; ++j) {
+      const float tj = quad_broadcast(s[j >> 2], j & 3);
 #pragma unroll
-      for (int i = row0(bt); i < row0(bt + 1); ++i) {
-        float s4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < (i + 3) / 4; ++q) {
-          const floatx4 a4 = rows[n++];
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (4 * q + e < i) s4[e] = fmaf(a4[e], t[4 * q + e], s4[e]);
-        }
-        const float sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-        t[i] = (i > cc) ? -sum : t[i];
-      }
+      for (int k = j >> 2; k < 4; ++k) s[k] = fmaf(-arow[k][j >> 2][j & 3], tj, s[k]);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) Ts[(16 * r + i) * CP + 16 * r + cc] = t[i];
+    for (int k = 0; k < 4; ++k) Ts[(16 * r + 4 * k + p) * CP + 16 * r + cc] = s[k];
   }
   lds_barrier();
   if (w < 2) {   // T10 (wave 0), T32 (wave 1)
