@@ -15,18 +15,10 @@
 #include "pf_scan_split.h"
 #include "pf_scan_split_f32.h"
 
-// loader waves of the split scan kernel for 32-column and for 16-column slices
-#ifndef PF_F32_SPLIT
-#define PF_F32_SPLIT 2
-#endif
-#ifndef PF_SPLIT_LW
-#define PF_SPLIT_LW 4
-#endif
-#ifndef PF_SPLIT16_LW
-#define PF_SPLIT16_LW 4
-#endif
-
 namespace {
+
+// loader waves of the bf16 split scan kernel for 32-column and for 16-column slices
+constexpr int kSplitLoaderWaves = 4, kSplit16LoaderWaves = 4;
 
 using pf::bf16;
 
@@ -130,13 +122,14 @@ void scan_output_launch(const void* q, const void* k, const void* v, const float
     // CUs idle (fewer than 8 chains per 32 CUs: long sequences at small batch); four MFMA waves
     // split every chunk (pf_scan_split.h)
     if ((size_t)BH * (DV / 32) < (size_t)device_cu_count())
-      pf::scan_split_kernel<C, DK, DV, 1, PF_SPLIT16_LW>
-          <<<dim3((unsigned)(BH * (DV / 16))), dim3(64 * (4 + PF_SPLIT16_LW)), 0, stream>>>(a);
+      pf::scan_split_kernel<C, DK, DV, 1, kSplit16LoaderWaves>
+          <<<dim3((unsigned)(BH * (DV / 16))), dim3(64 * (4 + kSplit16LoaderWaves)), 0, stream>>>(a);
     else
-      pf::scan_split_kernel<C, DK, DV, 2, PF_SPLIT_LW>
-          <<<dim3((unsigned)(BH * (DV / 32))), dim3(64 * (4 + PF_SPLIT_LW)), 0, stream>>>(a);
-  } else if (PF_F32_SPLIT == 1 || (PF_F32_SPLIT == 2 && (size_t)BH * (DV / 16) <= (size_t)device_cu_count())) {
-    // fp32, few chains: every chunk split over four waves (pf_scan_split_f32.h)
+      pf::scan_split_kernel<C, DK, DV, 2, kSplitLoaderWaves>
+          <<<dim3((unsigned)(BH * (DV / 32))), dim3(64 * (4 + kSplitLoaderWaves)), 0, stream>>>(a);
+  } else if ((size_t)BH * (DV / 16) <= (size_t)device_cu_count()) {
+    // fp32, at most one (chain, 16-column) slice per CU: every chunk split over four waves
+    // (pf_scan_split_f32.h); beyond that the two-wave kernel's 32-column slices fill the CUs better
     pf::scan_split_f32_kernel<C, DK, DV><<<dim3((unsigned)(BH * (DV / 16))), dim3(256), 0, stream>>>(a);
   } else {
     // fp32: transposed tiles staged by the loader; one LDS buffer (the images are 143 KB)
