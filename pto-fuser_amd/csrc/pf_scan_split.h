@@ -27,8 +27,10 @@
 // state is published and the chunk's stage buffer released (B3).  Per wave and chunk: 16 MFMAs
 // for k S and q S, 2 or 4 for T r, 2 or 4 for P v_new, 8 for the update (NT = 2), and 8 or 12
 // for the score: its ten 16x16 tiles (4 MFMAs each) are formed in phase B from the staged k and
-// q rows, three, three, two and two per wave so that the phase carries the same number of
-// products on every wave; the tiles (2,0), (3,0) and (3,1) reach their owners through PX.  P
+// q rows (a wave's own blocks from its registers), three, three, two and two per wave so that the
+// phase carries the same number of products on every wave; the tiles (2,0), (3,0) and (3,1)
+// reach their owners through PX.  Their gates come from two small tables the loader writes per
+// chunk (no exponential in the compute waves unless G rises or a block decays steeply).  P
 // never goes through HBM, and stage 1 reads no q.
 //
 // NLW loader waves (the rest of the workgroup) own the loads: chunk c+3's loads issued while the
@@ -36,11 +38,13 @@
 // free half of a double-buffered LDS stage (k and q rows swizzled for the permuted-K operand
 // reads and the transposed k^T reads, T rows, the v tile row-major, per-token gate tables).
 // Both are spread over the three phases of the interval (k's loads and LDS rows in the first,
-// T's and q's loads and T's rows in the second, v, the gates and q's rows in the third), and the
+// T's and q's loads, T's rows and the score gates in the second, v, the per-token gates and q's
+// rows in the third), and the
 // loader waves run at the default wave priority: a burst of loads or LDS writes issued at once,
 // or at a raised priority, was measured to stall the compute waves sharing the SIMDs (one phase
 // lost up to 1 000 cycles; q's loads in the first phase beside k's cost 5 % of the kernel).
-// The compute waves store their o rows themselves, one 16-byte store per lane and column block.  The loaders also carry the deferred state decay: the compute waves hold
+// The compute waves store their o rows themselves, one non-temporal 16-byte store per lane and
+// column block.  The loaders also carry the deferred state decay: the compute waves hold
 // S~ = S / f with a running factor f folded into the gate tables, and multiply it back only when
 // the loader flags a renormalisation (f below e^-60, or the last chunk, so the final state is
 // exact).
