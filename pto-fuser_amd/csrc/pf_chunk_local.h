@@ -229,7 +229,9 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
   floatx4 acc[N];
 #pragma unroll
   for (int b = 0; b < N; ++b) acc[b] = zero4();
-#pragma unroll
+  // unrolled by two, not fully: with every K step's operand reads hoisted the kernel needs 72
+  // VGPRs (seven waves per SIMD); by two it needs 61 and eight workgroups fit a CU
+#pragma unroll 2
   for (int kb = 0; kb < DK / Mfma<E>::KB; ++kb) {
 #pragma unroll
     for (int b = 0; b < N; ++b) {
@@ -277,10 +279,12 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
   }
 }
 
-// One workgroup per chunk; eight workgroups fit a CU for bf16 without P (four with P or fp32),
-// so the HBM latency of one chunk's loads overlaps the other workgroups' products and inverse.
+// One workgroup per chunk; eight workgroups fit a CU for bf16 without P (at most 64 VGPRs and
+// 17.9 KB of LDS each; four with P or fp32, which the LDS limits), so the HBM latency of one
+// chunk's loads overlaps the other workgroups' products and inverse.  At the headline's 16 chunks
+// per CU that is two generations of workgroups instead of three.
 template <typename E, typename TO, int C, int DK, bool DO_P, bool DO_INV>
-__global__ __launch_bounds__(256) void chunk_local_kernel(ChunkLocalArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void chunk_local_kernel(ChunkLocalArgs a) {
   static_assert(C == 64, "the chunk-local kernel is written for 64-token chunks");
   static_assert(DK % Mfma<E>::KB == 0, "head dim must be a multiple of the MFMA K block");
   constexpr int PE = 16 / sizeof(E);
