@@ -55,7 +55,8 @@ const char* pf_source_hash(void);
  *   q, k [B,H,T,DK] dtype; v [B,H,T,DV] dtype; beta, g [B,H,T] fp32 (g = per-token log decay,
  *   summed within each chunk of C tokens by the kernel); h0 [B,H,DK,DV] fp32 or NULL (zero);
  *   o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV] fp32 or NULL.
- *   Supported: C = 64 or 128, DK = DV = 128, T % C == 0.  The kernels run 64-token chunks; C = 128
+ *   Supported: C = 64 or 128, DK = DV = 128, T % C == 0, T <= 4 194 304 (per-chain addressing is
+ *   32-bit; a longer sequence is PF_ERR_ARG).  The kernels run 64-token chunks; C = 128
  *   (the reference's chunk) is served by them over T / 64 chunks — the chunked forward's result
  *   does not depend on the chunk size, only the blocking of its arithmetic does.
  * ------------------------------------------------------------------------------------------ */
@@ -118,7 +119,8 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
  *   h0 [B,H,DK,DV] fp32 or NULL; o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV]
  *   fp32 or NULL.  Supported: dtype PF_DTYPE_BF16 (bf16 MFMA, T >= 128) or PF_DTYPE_F32 (fp32
  *   operands and fp32 MFMA throughout, T >= 64), C = 64 or 128 (run as 64-token chunks),
- *   DK = DV = 128, T % C == 0.  The workspace holds the stage-1 images in the operand type.
+ *   DK = DV = 128, T % C == 0, T <= 4 194 304.  The workspace holds the stage-1 images in the
+ *   operand type.
  * ------------------------------------------------------------------------------------------ */
 size_t pf_kda_workspace_bytes(int B, int H, int T, int C, int DK, int DV, int dtype);
 void* pf_kda_setup(int B, int H, int T, int C, int DK, int DV, int dtype);

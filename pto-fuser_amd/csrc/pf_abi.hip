@@ -53,8 +53,8 @@ struct GdnLayout {
 constexpr int kChunk = 64;
 
 bool gdn_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
-  return B > 0 && H > 0 && T > 0 && (C == 64 || C == 128) && DK == 128 && DV == 128 &&
-         T % C == 0 && valid_dtype(dtype);
+  return B > 0 && H > 0 && T > 0 && T <= pf::kMaxChainTokens && (C == 64 || C == 128) && DK == 128 &&
+         DV == 128 && T % C == 0 && valid_dtype(dtype);
 }
 
 template <typename E>

@@ -12,6 +12,11 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 // Cache-policy operand of the raw buffer builtins for a non-temporal (streaming) access.
 constexpr int kCachePolicyNT = 2;
 
+// Longest chain (tokens of one (b, h)) the entry points accept: a chain's o rows (T x 128 fp32)
+// are addressed through one buffer descriptor, whose byte range and offsets are 32-bit; the limit
+// keeps them below 2^31.
+constexpr int kMaxChainTokens = 1 << 22;
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }

@@ -41,8 +41,8 @@ struct KdaLayout {
 constexpr int kChunk = 64;
 
 bool kda_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
-  return B > 0 && H > 0 && T > 0 && (C == 64 || C == 128) && DK == 128 && DV == 128 &&
-         T % C == 0 &&
+  return B > 0 && H > 0 && T > 0 && T <= pf::kMaxChainTokens && (C == 64 || C == 128) &&
+         DK == 128 && DV == 128 && T % C == 0 &&
          ((dtype == PF_DTYPE_BF16 && T / kChunk >= 2) || dtype == PF_DTYPE_F32);
 }
 

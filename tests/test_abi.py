@@ -72,6 +72,11 @@ def test_workspace_sizing_contract(lib):
     assert lib.pf_gdn_workspace_bytes(1, 1, 128, 32, 128, 128, 1) == 0      # C != 64
     assert lib.pf_gdn_workspace_bytes(1, 1, 128, 64, 64, 128, 1) == 0       # DK != 128
     assert lib.pf_gdn_workspace_bytes(1, 1, 128, 64, 128, 128, 7) == 0      # bad dtype
+    # the longest chain: 2^22 tokens (32-bit per-chain addressing); one chunk more is refused
+    assert lib.pf_gdn_workspace_bytes(1, 1, 1 << 22, 64, 128, 128, 1) > 0
+    assert lib.pf_gdn_workspace_bytes(1, 1, (1 << 22) + 64, 64, 128, 128, 1) == 0
+    assert lib.pf_gdn_exec(None, None, None, None, None, None, None, None, 1, 1, (1 << 22) + 64, 64,
+                           128, 128, 1, 0.1, None, None) == _hip.PF_ERR_ARG
     assert not lib.pf_gdn_setup(1, 1, 100, 64, 128, 128, 1)
 
 
@@ -89,6 +94,8 @@ def test_kda_workspace_and_rejects(lib):
     assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_F32) > 0     # one chunk
     assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_BF16) == 0    # bf16: two
     assert not lib.pf_kda_setup(1, 1, 100, 64, 128, 128, 1)
+    assert lib.pf_kda_workspace_bytes(1, 1, 1 << 22, 64, 128, 128, 1) > 0
+    assert lib.pf_kda_workspace_bytes(1, 1, (1 << 22) + 64, 64, 128, 128, 1) == 0
     assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
                            1, 0.1, None, None) == _hip.PF_ERR_WORKSPACE
     assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
