@@ -60,6 +60,10 @@ __device__ __forceinline__ void lds_barrier() {
   __asm__ __volatile__("" ::: "memory");
 }
 
+// Index of the lower-triangular 16x16 tile (ib, jb), jb <= ib, of a 64 x 64 chunk matrix (T, the
+// score) in a packed list of its ten tiles.
+__device__ __forceinline__ constexpr int score_tile_index(int ib, int jb) { return ib * (ib + 1) / 2 + jb; }
+
 // exp(x) for x <= 0, 0 for x > 0 (the reference's _safe_exp).
 __device__ __forceinline__ float safe_exp(float x) { return x <= 0.f ? __expf(x) : 0.f; }
 

@@ -77,9 +77,6 @@ struct SplitStage {
                   // [2] nonzero: the score gates are evaluated per element (CB, RA not valid)
 };
 
-// Index of the lower-triangular 16x16 score tile (ib, jb), jb <= ib, in Stage::RA.
-__device__ __forceinline__ constexpr int score_tile_index(int ib, int jb) { return ib * (ib + 1) / 2 + jb; }
-
 // Decay inside one 16-token block (G at its start minus G at its end) up to which the factored
 // score gate e^{G_i - G_j} = e^{G_i - G_m} e^{G_m - G_j} is used: its key factor stays below e^80.
 constexpr float kScoreGateSpan = 80.f;

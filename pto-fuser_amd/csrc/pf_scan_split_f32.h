@@ -12,8 +12,11 @@
 //      S_w <- e^{G_last} S_w + k[:, rows of w]^T (e^{G_last - G} v_new)
 //
 // so the chain carries 64 + 40 + 32 products per wave per chunk instead of one wave's ~460.  The
-// next chunk's k, q, T, P, v and gates are loaded into registers while a chunk is computed and
-// written into the (single) LDS image between two barriers.
+// next chunk is loaded into registers while a chunk is computed.  q is last read in step 1, and
+// T and P (kept as their ten lower 16x16 tiles, in two buffers) are read from the current buffer
+// in step 2, so the next chunk's q, T and P are written into LDS during step 2, and its q, T and
+// P loads for the chunk after issued then; only k (read by step 2's update), v and the gate
+// tables are written between the two barriers that end a chunk.
 #pragma once
 
 #include "pf_scan_output.h"
@@ -24,12 +27,16 @@ template <int C, int DK, int DV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void scan_split_f32_kernel(ScanOutArgs a) {
   static_assert(C == 64 && DK == 128 && DV % 16 == 0, "tile shapes of the fp32 split scan: C 64, DK 128");
-  constexpr int KP = DK + 4, TP = C + 4, VP = 16 + 4;
+  constexpr int KP = DK + 4, VP = 16 + 4;
   constexpr int NK = C * DK / 4 / 256, NT = C * C / 4 / 256;   // float4 copies per thread
+  // T and P as their ten lower-triangular 16x16 tiles, tile (ib, jb) at score_tile_index(ib, jb),
+  // rows padded to 20 floats; two buffers, so a chunk's tiles are written while the previous
+  // chunk's are read
+  constexpr int TR = 20, TT = 16 * TR, TB = 10 * TT;
   __shared__ __attribute__((aligned(16))) float ks[C * KP];
   __shared__ __attribute__((aligned(16))) float qs[C * KP];
-  __shared__ __attribute__((aligned(16))) float ts[C * TP];
-  __shared__ __attribute__((aligned(16))) float ps[C * TP];
+  __shared__ __attribute__((aligned(16))) float tsb[2][TB];
+  __shared__ __attribute__((aligned(16))) float psb[2][TB];
   __shared__ __attribute__((aligned(16))) float vs[C * VP];
   __shared__ __attribute__((aligned(16))) float Bs[C], BEG[C], EG[C], EL[C], DL[4];
   __shared__ __attribute__((aligned(16))) floatx4 YP[4 * 4 * 64];   // [wave][token tile][lane]
@@ -51,12 +58,13 @@ void scan_split_f32_kernel(ScanOutArgs a) {
   // ---- one chunk: global -> registers -> LDS ----
   floatx4 rk[NK], rq[NK], rt[NT], rp[NT], rv;
   float rg = 0.f, rb = 0.f;
-  auto load = [&](int ch) {
+  // thread tid holds T / P rows 16 i + tid / 16, columns 4 (tid % 16) .. : tile (i, (tid % 16) / 4)
+  const int t_row = tid >> 4, t_jb = (tid & 15) >> 2, t_col = 4 * (tid & 3);
+  auto load_qtp = [&](int ch) {
     const size_t t0 = (size_t)ch * C;
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
       const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
-      rk[i] = *reinterpret_cast<const floatx4*>(kb + (t0 + row) * DK + 4 * q4);
       rq[i] = *reinterpret_cast<const floatx4*>(qb + (t0 + row) * DK + 4 * q4);
     }
 #pragma unroll
@@ -64,6 +72,31 @@ void scan_split_f32_kernel(ScanOutArgs a) {
       const int u = tid + 256 * i, row = u >> 4, q4 = u & 15;
       rt[i] = *reinterpret_cast<const floatx4*>(tb + ((size_t)ch * C + row) * C + 4 * q4);
       rp[i] = *reinterpret_cast<const floatx4*>(pb + ((size_t)ch * C + row) * C + 4 * q4);
+    }
+  };
+  auto store_qtp = [&](int ch) {
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
+      *reinterpret_cast<floatx4*>(qs + row * KP + 4 * q4) = rq[i];
+    }
+    float* tsd = tsb[ch & 1];
+    float* psd = psb[ch & 1];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      if (t_jb <= i) {
+        const int off = score_tile_index(i, t_jb) * TT + t_row * TR + t_col;
+        *reinterpret_cast<floatx4*>(tsd + off) = rt[i];
+        *reinterpret_cast<floatx4*>(psd + off) = rp[i];
+      }
+    }
+  };
+  auto load = [&](int ch) {
+    const size_t t0 = (size_t)ch * C;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
+      rk[i] = *reinterpret_cast<const floatx4*>(kb + (t0 + row) * DK + 4 * q4);
     }
     rv = *reinterpret_cast<const floatx4*>(vb + (t0 + (tid >> 2)) * DV + col0 + 4 * (tid & 3));
     if (tid < C) {
@@ -76,13 +109,6 @@ void scan_split_f32_kernel(ScanOutArgs a) {
     for (int i = 0; i < NK; ++i) {
       const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
       *reinterpret_cast<floatx4*>(ks + row * KP + 4 * q4) = rk[i];
-      *reinterpret_cast<floatx4*>(qs + row * KP + 4 * q4) = rq[i];
-    }
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const int u = tid + 256 * i, row = u >> 4, q4 = u & 15;
-      *reinterpret_cast<floatx4*>(ts + row * TP + 4 * q4) = rt[i];
-      *reinterpret_cast<floatx4*>(ps + row * TP + 4 * q4) = rp[i];
     }
     *reinterpret_cast<floatx4*>(vs + (tid >> 2) * VP + 4 * (tid & 3)) = rv;
     if (w == 0) {                                     // lane = token
@@ -103,9 +129,14 @@ void scan_split_f32_kernel(ScanOutArgs a) {
       S[r][ii] = a.h0 ? a.h0[((size_t)bh * DK + 32 * w + 16 * r + 4 * g + ii) * DV + col0 + c] : 0.f;
 
   load(0);
+  load_qtp(0);
   store();
+  store_qtp(0);
   lds_barrier();
-  if (NC > 1) load(1);
+  if (NC > 1) {
+    load(1);
+    load_qtp(1);
+  }
 
   for (int ch = 0; ch < NC; ++ch) {
     // ---- 1. partial products over this wave's 32 state rows ----
@@ -126,6 +157,13 @@ void scan_split_f32_kernel(ScanOutArgs a) {
       QP[(w * 4 + ib) * 64 + lane] = qy;
     }
     lds_barrier();
+    // q of this chunk is read: the next chunk's q, and its T and P into the other buffer
+    if (ch + 1 < NC) {
+      store_qtp(ch + 1);
+      if (ch + 2 < NC) load_qtp(ch + 2);
+    }
+    const float* ts = tsb[ch & 1];
+    const float* ps = psb[ch & 1];
     // ---- 2. r, v_new = T r for all tokens; o for tokens 16w ..; the update of rows 32w .. ----
     floatx4 VN[4];
 #pragma unroll
@@ -148,7 +186,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
         floatx4 acc = zero4();
 #pragma unroll
         for (int jb = 0; jb <= ib; ++jb) {
-          const floatx4 ta = *reinterpret_cast<const floatx4*>(ts + (16 * ib + c) * TP + 16 * jb + 4 * g);
+          const floatx4 ta = *reinterpret_cast<const floatx4*>(ts + score_tile_index(ib, jb) * TT + c * TR + 4 * g);
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[ii], VN[jb][ii], acc, 0, 0, 0);
         }
@@ -164,7 +202,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[16 * w + 4 * g + ii];
       for (int jb = 0; jb <= w; ++jb) {
-        const floatx4 pa = *reinterpret_cast<const floatx4*>(ps + (16 * w + c) * TP + 16 * jb + 4 * g);
+        const floatx4 pa = *reinterpret_cast<const floatx4*>(ps + score_tile_index(w, jb) * TT + c * TR + 4 * g);
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) O = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ii], VN[jb][ii], O, 0, 0, 0);
       }
