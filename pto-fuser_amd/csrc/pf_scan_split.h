@@ -81,12 +81,12 @@ struct SplitStage {
 // score gate e^{G_i - G_j} = e^{G_i - G_m} e^{G_m - G_j} is used: its key factor stays below e^80.
 constexpr float kScoreGateSpan = 80.f;
 
-// Loader register image of one chunk (k, q: 1024 16-byte vectors; T, P: 512; v: 8 NCOL).
+// Loader register image of one chunk (k, q: 1024 16-byte vectors each; T: 512; v: 8 NCOL).
 template <int NLW, int NCOL>
 struct SplitRegs {
-  static constexpr int NK = 1024 / (64 * NLW), NTP = 512 / (64 * NLW);
+  static constexpr int NK = 1024 / (64 * NLW), NTR = 512 / (64 * NLW);
   static constexpr int NV = (8 * NCOL + 64 * NLW - 1) / (64 * NLW);
-  uint4 k[NK], q[NK], t[NTP], v[NV];
+  uint4 k[NK], q[NK], t[NTR], v[NV];
   float g, b;
 };
 
@@ -146,13 +146,13 @@ void scan_split_kernel(ScanOutArgs a) {
       return NLW == 2 ? ((i & 1) << 2) | (((i >> 1) & 1) << 4) | (((i >> 2) & 1) << 5)
                       : ((i & 1) << 2) | (((i >> 1) & 1) << 5);
     };
-    // T / P rows (8 vectors per row): vec = lt & 7, a = lt >> 3
+    // T rows (8 vectors per row): vec = lt & 7, a = lt >> 3
     //   NLW 2: row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | i1<<5
     //   NLW 4: row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | a4<<5
     const int ta = lt >> 3, tvec = lt & 7;
     const int trow_l = (ta & 7) | ((ta >> 3) << 4);
-    const uint32_t tp_voff = (uint32_t)(trow_l * C + tvec * 8) * 2;
-    const int tp_lds = trow_l * TP + 8 * tvec;
+    const uint32_t t_voff = (uint32_t)(trow_l * C + tvec * 8) * 2;
+    const int t_lds = trow_l * TP + 8 * tvec;
     auto trow_i = [](int i) -> int { return NLW == 2 ? ((i & 1) << 3) | (((i >> 1) & 1) << 5) : ((i & 1) << 3); };
     // v tile (NCOL / 8 vectors per row): vector u = lt + 64 NLW i; lanes past the tile's vectors
     // repeat one (load only)
@@ -179,12 +179,12 @@ void scan_split_kernel(ScanOutArgs a) {
         r.q[i] = buf_load16(rq, kq_voff, kq_s + rowi * DK * 2);
       }
     };
-    auto load_tp = [&](Regs& r, int ch) {
-      const uint32_t tp_s = (uint32_t)ch * C * C * 2;
+    auto load_t = [&](Regs& r, int ch) {
+      const uint32_t t_s = (uint32_t)ch * C * C * 2;
 #pragma unroll
-      for (int i = 0; i < Regs::NTP; ++i) {
+      for (int i = 0; i < Regs::NTR; ++i) {
         const uint32_t rowi = trow_i(i);
-        r.t[i] = buf_load16(rt, tp_voff, tp_s + rowi * C * 2);
+        r.t[i] = buf_load16(rt, t_voff, t_s + rowi * C * 2);
       }
     };
     auto load_vg = [&](Regs& r, int ch) {
@@ -205,11 +205,11 @@ void scan_split_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int i = 0; i < Regs::NK; ++i) put16(s.qs + kq_lds + krow_i(i) * KP, r.q[i], (i & 1) != 0);
     };
-    auto store_tp = [&](Stage& s, const Regs& r) {
+    auto store_t = [&](Stage& s, const Regs& r) {
 #pragma unroll
-      for (int i = 0; i < Regs::NTP; ++i) {
+      for (int i = 0; i < Regs::NTR; ++i) {
         const int rowi = trow_i(i);
-        put16(s.ts + tp_lds + rowi * TP, r.t[i], (i & 1) != 0);
+        put16(s.ts + t_lds + rowi * TP, r.t[i], (i & 1) != 0);
       }
     };
     auto store_vg = [&](Stage& s, const Regs& r, int ch) {
@@ -284,9 +284,9 @@ void scan_split_kernel(ScanOutArgs a) {
       load_kq(ld, nl);
       store_k(sn, nx);
       lds_barrier();                                     // B1
-      load_tp(ld, nl);
+      load_t(ld, nl);
       load_q(ld, nl);
-      store_tp(sn, nx);
+      store_t(sn, nx);
       store_gates(sn, nx);
       lds_barrier();                                     // B2
       load_vg(ld, nl);
@@ -301,19 +301,19 @@ void scan_split_kernel(ScanOutArgs a) {
     };
     load_kq(r0, 0);
     load_q(r0, 0);
-    load_tp(r0, 0);
+    load_t(r0, 0);
     load_vg(r0, 0);
     load_kq(r1, min(1, last));
     load_q(r1, min(1, last));
-    load_tp(r1, min(1, last));
+    load_t(r1, min(1, last));
     load_vg(r1, min(1, last));
     load_kq(r2, min(2, last));
     load_q(r2, min(2, last));
-    load_tp(r2, min(2, last));
+    load_t(r2, min(2, last));
     load_vg(r2, min(2, last));
     store_k(st[0], r0);
     store_q(st[0], r0);
-    store_tp(st[0], r0);
+    store_t(st[0], r0);
     store_gates(st[0], r0);
     store_vg(st[0], r0, 0);
     lds_barrier();                                       // start: stage 0 and SB ready
@@ -338,7 +338,7 @@ void scan_split_kernel(ScanOutArgs a) {
     // per-lane LDS element offsets
     const int kq_rd = (tok0 + c) * KP + 4 * (g ^ ((c >> 2) & 3));          // k / q rows
     const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g) + 32 * cw; // k^T, rows 32cw..
-    const int tp_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // T rows
+    const int t_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // T rows
     const int kj_rd = c * KP + 4 * (g ^ ((c >> 2) & 3));                   // k / q rows 16 b + c
     const float oscale = *a.scale;
     const int v_rd = (tok0 + 4 * g + (c >> 2)) * VP + 4 * (c & 3);         // v, transposed read
@@ -401,7 +401,7 @@ void scan_split_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         if (kb == 0 || cw >= 2) {
-          const bf16* tp = s.ts + tp_rd + 32 * kb;
+          const bf16* tp = s.ts + t_rd + 32 * kb;
           const bf16x8 ta = cat8(*reinterpret_cast<const bf16x4*>(tp), *reinterpret_cast<const bf16x4*>(tp + 16));
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt)
