@@ -57,6 +57,19 @@ bool gdn_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
          DV == 128 && T % C == 0 && valid_dtype(dtype);
 }
 
+// CUs of the device current at the first call (queried once, thread-safe; 256, MI355X's count,
+// if the query fails).
+int device_cu_count() {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      return n;
+    return 256;
+  }();
+  return cus;
+}
+
 template <typename E>
 void chunk_local_launch(const void* q, const void* k, const float* beta, const float* g,
                        float scale, char* base, size_t M, hipStream_t stream) {
@@ -76,24 +89,15 @@ void chunk_local_launch(const void* q, const void* k, const float* beta, const f
   a.t_lower_only = 1;   // the scan kernels read T's rows 0..31 up to column 31 only
   a.p_scale = scale;
   a.scale_out = reinterpret_cast<float*>(base + lay.s_off);
-  if constexpr (std::is_same<E, bf16>::value)   // no P: the bf16 scan forms it from its q, k rows
+  if constexpr (std::is_same<E, bf16>::value) {   // no P: the bf16 scan forms it from its q, k rows
     pf::chunk_local_kernel<E, E, C, DK, false, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
-  else
-    pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3((unsigned)M), dim3(256), 0, stream>>>(a);
-}
-
-// CUs of the current device (queried once; 256 on MI355X if the query fails).
-int device_cu_count() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      cus = n;
-    else
-      cus = 256;
+  } else {
+    // fp32 with P: when the chunks fit one generation of workgroups (short sequences, few
+    // chains), P gets workgroups of its own, which halves each workgroup's products
+    a.split_p = M <= (size_t)device_cu_count() ? 1 : 0;
+    const unsigned grid = (unsigned)(a.split_p ? 2 * M : M);
+    pf::chunk_local_kernel<E, E, C, DK, true, true><<<dim3(grid), dim3(256), 0, stream>>>(a);
   }
-  return cus;
 }
 
 template <typename E>

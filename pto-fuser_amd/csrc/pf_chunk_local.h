@@ -16,6 +16,8 @@
 // (16x16x4), the product chains kept in registers through the permuted-K layout.
 #pragma once
 
+#include <type_traits>
+
 #include "pf_device.h"
 
 // Barriers are LDS-only (lds_barrier): waves exchange data through LDS alone, so a barrier need
@@ -38,6 +40,9 @@ struct ChunkLocalArgs {
                         //    unwritten: the fused forward's scan never reads it
   float p_scale;        // multiplies P (the forward's output scale)
   float* scale_out;     // if set, block 0 records p_scale here for the scan stage
+  int split_p;          // with P: 1 = grid of 2M blocks, blocks M .. 2M-1 form P of chunk b - M
+                        //    alone and blocks 0 .. M-1 the rest (half the products per block,
+                        //    for launches whose M blocks would leave most CUs idle)
 };
 
 // (I + A)^-1 of one strictly-lower C x C block held in LDS (As, fp32, pitch C+4) into Ts (same
@@ -201,30 +206,36 @@ __device__ __forceinline__ void unit_lower_inverse64(float* As, float* Ts) {
 // block of A (k rows i against k rows j).  The lists group each wave's blocks by shared rows, so
 // a wave reads every 16-row operand block it needs once per K step and feeds it to all of its
 // MFMAs (with P: 18 operand reads per K step for the workgroup instead of 40):
-//   with P   w0: A row 3 + P(0,0)   w1: P row 3 + A(0,0)   w2: A rows 1-2   w3: P rows 1-2
+//   A and P  w0: A row 3 + P(0,0)   w1: P row 3 + A(0,0)   w2: A rows 1-2   w3: P rows 1-2
 //   A only   w0: A(3,0..1)   w1: A row 2   w2: A row 1 + A(0,0)   w3: A(3,2..3)
-__device__ __forceinline__ constexpr int score_count(bool do_p, int w) {
-  return do_p ? 5 : ((w == 0 || w == 3) ? 2 : 3);
+//   P only   w0: P(3,0..2)   w1: P(2,0..2)   w2: P row 1   w3: P(0,0) + P(3,3)
+enum ScoreSet : int { kScoreA = 0, kScoreAP = 1, kScoreP = 2 };
+__device__ __forceinline__ constexpr int score_count(int set, int w) {
+  return set == kScoreAP ? 5 : (set == kScoreA ? ((w == 0 || w == 3) ? 2 : 3) : (w < 2 ? 3 : 2));
 }
-__device__ __forceinline__ constexpr int score_code(bool do_p, int w, int b) {
-  return do_p ? (w == 0   ? (b < 4 ? 12 + b : 16)
-                 : w == 1 ? (b < 4 ? 16 + 12 + b : 0)
-                 : w == 2 ? (b < 2 ? 4 + b : 8 + (b - 2))
-                          : 16 + (b < 2 ? 4 + b : 8 + (b - 2)))
-              : (w == 0   ? 12 + b
-                 : w == 1 ? 8 + b
-                 : w == 2 ? (b < 2 ? 4 + b : 0)
-                          : 14 + b);
+__device__ __forceinline__ constexpr int score_code(int set, int w, int b) {
+  return set == kScoreAP ? (w == 0   ? (b < 4 ? 12 + b : 16)
+                            : w == 1 ? (b < 4 ? 16 + 12 + b : 0)
+                            : w == 2 ? (b < 2 ? 4 + b : 8 + (b - 2))
+                                     : 16 + (b < 2 ? 4 + b : 8 + (b - 2)))
+       : set == kScoreA  ? (w == 0   ? 12 + b
+                            : w == 1 ? 8 + b
+                            : w == 2 ? (b < 2 ? 4 + b : 0)
+                                     : 14 + b)
+                         : 16 + (w == 0   ? 12 + b
+                                 : w == 1 ? 8 + b
+                                 : w == 2 ? 4 + b
+                                          : (b == 0 ? 0 : 15));
 }
 
 // One wave's score blocks: products, then (after the workgroup barrier that frees the k / q
 // tiles) the gate / mask epilogue.  Each product is formed transposed —
 // D[4g+ii][c] = sum_d k[j][d] x[i][d] with i = 16 bi + c, j = 16 bj + 4g + ii — so a lane holds
 // four consecutive columns of one score row and stores them as one vector.
-template <typename E, int C, int DK, int KP, int CP, bool DO_P, int W>
+template <typename E, int C, int DK, int KP, int CP, int SET, int W>
 __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks, const E* qs,
                                            float* As, const float* Gs, const float* Bs, int m) {
-  constexpr int N = score_count(DO_P, W);
+  constexpr int N = score_count(SET, W);
   const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   floatx4 acc[N];
 #pragma unroll
@@ -235,7 +246,7 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
   for (int kb = 0; kb < DK / Mfma<E>::KB; ++kb) {
 #pragma unroll
     for (int b = 0; b < N; ++b) {
-      const int code = score_code(DO_P, W, b);
+      const int code = score_code(SET, W, b);
       const E* jrow = ks + (16 * (code & 3) + c) * KP;
       const E* irow = ((code & 16) ? qs : ks) + (16 * ((code >> 2) & 3) + c) * KP;
       acc[b] = Mfma<E>::rows(acc[b], jrow, irow, kb, g);   // equal rows: one LDS read
@@ -247,7 +258,7 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
   // around the exponential), so no lane-divergent branch splits the wave's instruction stream.
 #pragma unroll
   for (int b = 0; b < N; ++b) {
-    const int code = score_code(DO_P, W, b);
+    const int code = score_code(SET, W, b);
     const int i = 16 * ((code >> 2) & 3) + c, j0 = 16 * (code & 3) + 4 * g;
     const float gi = Gs[i];
     const floatx4 gj = *reinterpret_cast<const floatx4*>(Gs + j0);
@@ -271,7 +282,7 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
       store4(static_cast<E*>(a.P_out) + (size_t)m * C * C + i * C + j0, out[0], out[1], out[2], out[3]);
     }
   }
-  if (DO_P && (W == 0 || W == 3)) {
+  if (SET != kScoreA && (W == 0 || W == 3)) {
     // the strictly-upper blocks of P that the scan kernels read as parts of a 32-wide K block:
     // (0,1) beside P(0,0) (wave 0) and (2,3) beside P row 2 (wave 3); the other four are never read
     const int i = (W == 0 ? 0 : 32) + c, j0 = (W == 0 ? 16 : 48) + 4 * g;
@@ -309,11 +320,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   float* As = reinterpret_cast<float*>(kqt);
   float* Ts = As;
 
-  const int m = blockIdx.x;
+  // block role (block-uniform): P alone (split launch, second half of the grid), A, T and P in
+  // one block (DO_P, no split), or A and T (no P, or the first half of a split launch)
+  const bool p_only = DO_P && a.split_p && (int)blockIdx.x >= a.M;
+  const bool stage_q = DO_P && (p_only || !a.split_p);
+  const int m = p_only ? (int)blockIdx.x - a.M : (int)blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
   const size_t row0 = (size_t)m * C;
-  if (a.scale_out && m == 0 && tid == 0) *a.scale_out = a.p_scale;
+  if (a.scale_out && !p_only && m == 0 && tid == 0) *a.scale_out = a.p_scale;
 
   // ---- 1. stage k (and q), gates: every load issued before the first LDS store ----------------
   {
@@ -323,7 +338,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 #pragma unroll
     for (int i = 0; i < NVT; ++i) {
       kr[i] = kg[tid + 256 * i];
-      qr[i] = DO_P ? qg[tid + 256 * i] : u32x4{0u, 0u, 0u, 0u};
+      qr[i] = stage_q ? qg[tid + 256 * i] : u32x4{0u, 0u, 0u, 0u};
     }
     const float x = a.g != nullptr ? a.g[row0 + (tid & (C - 1))] : 0.f;
     const float bv = a.beta[row0 + (tid & (C - 1))];
@@ -332,7 +347,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       const int u = tid + 256 * i;
       const int r = u / (DK / VE), v = u % (DK / VE);
       *reinterpret_cast<u32x4*>(ks + r * KP + v * VE) = kr[i];
-      if (DO_P) *reinterpret_cast<u32x4*>(qs + r * KP + v * VE) = qr[i];
+      if (stage_q) *reinterpret_cast<u32x4*>(qs + r * KP + v * VE) = qr[i];
     }
     if (w == 0) {   // G = within-chunk cumsum of g (lane = token)
       float xs = x;
@@ -345,17 +360,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       }
       Gs[lane] = xs;
       Bs[lane] = bv;
-      if (a.G_out) a.G_out[row0 + lane] = xs;
+      if (a.G_out && !p_only) a.G_out[row0 + lane] = xs;
     }
   }
   lds_barrier();
 
-  // ---- 2. gated score blocks: kkt (A) and, optionally, qk (P) ------------------------------------
-  switch (w) {
-    case 0: score_wave<E, C, DK, KP, CP, DO_P, 0>(a, ks, qs, As, Gs, Bs, m); break;
-    case 1: score_wave<E, C, DK, KP, CP, DO_P, 1>(a, ks, qs, As, Gs, Bs, m); break;
-    case 2: score_wave<E, C, DK, KP, CP, DO_P, 2>(a, ks, qs, As, Gs, Bs, m); break;
-    default: score_wave<E, C, DK, KP, CP, DO_P, 3>(a, ks, qs, As, Gs, Bs, m); break;
+  // ---- 2. gated score blocks: kkt (A) and / or qk (P) ---------------------------------------------
+  auto scores = [&](auto set_tag) {
+    constexpr int SET = decltype(set_tag)::value;
+    switch (w) {
+      case 0: score_wave<E, C, DK, KP, CP, SET, 0>(a, ks, qs, As, Gs, Bs, m); break;
+      case 1: score_wave<E, C, DK, KP, CP, SET, 1>(a, ks, qs, As, Gs, Bs, m); break;
+      case 2: score_wave<E, C, DK, KP, CP, SET, 2>(a, ks, qs, As, Gs, Bs, m); break;
+      default: score_wave<E, C, DK, KP, CP, SET, 3>(a, ks, qs, As, Gs, Bs, m); break;
+    }
+  };
+  if constexpr (DO_P) {
+    if (p_only) {
+      scores(std::integral_constant<int, kScoreP>{});
+      return;                                          // the whole block: no barrier follows
+    }
+    if (a.split_p)
+      scores(std::integral_constant<int, kScoreA>{});
+    else
+      scores(std::integral_constant<int, kScoreAP>{});
+  } else {
+    scores(std::integral_constant<int, kScoreA>{});
   }
   lds_barrier();
 

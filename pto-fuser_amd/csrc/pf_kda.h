@@ -59,7 +59,7 @@ __device__ __forceinline__ int kda_swz(int r, int col) {
 template <int C, int KP, int CP, int W>
 __device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, const bf16* qt, float* As,
                                                const float* Bs, bf16* P) {
-  constexpr int N = score_count(true, W);
+  constexpr int N = score_count(kScoreAP, W);
   const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int rd = c * KP + 4 * (g ^ ((c >> 2) & 3));   // row c, K groups g and g+4 of each 32-block
   floatx4 acc[N];
@@ -69,7 +69,7 @@ __device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, c
   for (int kb = 0; kb < 128 / 32; ++kb) {
 #pragma unroll
     for (int b = 0; b < N; ++b) {
-      const int code = score_code(true, W, b);
+      const int code = score_code(kScoreAP, W, b);
       const bf16* jp = bt + 16 * (code & 3) * KP + rd + 32 * kb;
       const bf16* ip = ((code & 16) ? qt : at) + 16 * ((code >> 2) & 3) * KP + rd + 32 * kb;
       const bf16x8 ja = cat8(*reinterpret_cast<const bf16x4*>(jp), *reinterpret_cast<const bf16x4*>(jp + 16));
@@ -79,7 +79,7 @@ __device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, c
   }
 #pragma unroll
   for (int b = 0; b < N; ++b) {
-    const int code = score_code(true, W, b);
+    const int code = score_code(kScoreAP, W, b);
     const int i = 16 * ((code >> 2) & 3) + c, j0 = 16 * (code & 3) + 4 * g;
     floatx4 out;
     if (!(code & 16)) {

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void kda_local_f32_kernel(KdaLocalF32Args a) {
       for (int kb = 0; kb < DK / 16; ++kb) {
 #pragma unroll
         for (int b = 0; b < N; ++b) {
-          const int code = score_code(true, WW, b);
+          const int code = score_code(kScoreAP, WW, b);
           const float* jrow = bt + (16 * (code & 3) + c) * RP;
           const float* irow = ((code & 16) ? qt : at) + (16 * ((code >> 2) & 3) + c) * RP;
           acc[b] = Mfma<float>::rows(acc[b], jrow, irow, kb, g);
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void kda_local_f32_kernel(KdaLocalF32Args a) {
     // each product is formed transposed: acc[ii] = (x_i . b_j), i = 16 bi + c, j = 16 bj + 4g + ii
 #pragma unroll
     for (int b = 0; b < N; ++b) {
-      const int code = score_code(true, w, b);
+      const int code = score_code(kScoreAP, w, b);
       const int i = 16 * ((code >> 2) & 3) + c, j0 = 16 * (code & 3) + 4 * g;
       floatx4 out;
       if (!(code & 16)) {
