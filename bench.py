@@ -30,7 +30,8 @@ Besides the required fields the line carries:
     record was taken from the library built from the current sources (its source hash), else
     null;
   * ``stages`` — both kernels' average durations, bytes and flops, and their HBM / MFMA fractions;
-  * ``forward`` — the whole forward's compulsory-byte and flop fractions at ``ms_per_step``;
+  * ``forward`` — the whole forward's compulsory-byte and flop fractions at ``ms_per_step``,
+    and the timed loop run REPEATS more times (``repeats_ms_per_step``, their median);
   * ``cpu_baseline`` — the fp32 numpy oracle (the reference's per-(b,h,c) loop) on this host's
     cores (oracle/cpu_baseline.py), with a one-core figure beside it;
   * ``secondary`` — the other benchmark configurations, each timed over back-to-back calls
@@ -55,6 +56,7 @@ sys.path.insert(0, ROOT)
 
 WORKLOAD = dict(B=4, H=16, T=4096, C=64, DK=128, DV=128)
 SETTLE_S = 1.0      # untimed GPU work before the warmup steps (clock ramp)
+REPEATS = 5         # further runs of the timed loop, reported as a median beside `value`
 PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
 PEAK_BF16 = 2.5e15         # dense bf16 MFMA, flop/s
 PEAK_FP32 = 157.3e12       # dense fp32 MFMA, flop/s
@@ -439,6 +441,8 @@ def main(argv=None) -> int:
     e_end.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e_start.elapsed_time(e_end) / args.steps
+    # the same loop repeated REPEATS more times (reported beside the timed loop, not in `value`)
+    repeat_ms = [_event_ms(step, args.steps, 0) for _ in range(REPEATS)]
 
     # per-kernel durations, after the timed loop: ``--event-steps`` forwards and as many stage-1
     # launches, each run back to back under one event pair on the launch stream.  Stage 1's
@@ -504,7 +508,9 @@ def main(argv=None) -> int:
                     "own_bytes": total_bytes, "own_hbm_frac": round(total_bytes / fs / PEAK_HBM, 4),
                     "flops": total_flops,
                     "mfma_bf16_frac": round(total_flops / fs / PEAK_BF16, 4),
-                    "event_steps": args.event_steps},
+                    "event_steps": args.event_steps,
+                    "repeats_ms_per_step": [round(x, 5) for x in repeat_ms],
+                    "repeats_median_ms": round(statistics.median(repeat_ms), 5)},
     }
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4

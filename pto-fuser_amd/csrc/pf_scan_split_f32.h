@@ -6,17 +6,21 @@
 // state rows 32w .. 32w+31 (fp32, MFMA D layout, in registers for the whole chain).  Per chunk
 // (T, P, G from stage 1; fp32 MFMA 16x16x4 throughout):
 //
-//   1. partial Y_w = k[:, rows of w] S_w and (q S)_w for all 64 tokens     -> LDS
-//   2. every wave: Y = sum of the partials, r = beta v - beta e^G Y, v_new = T r (all tokens);
-//      wave w: o for tokens 16w .. 16w+15 = scale e^G (sum of the q S partials) + P v_new -> HBM;
-//      S_w <- e^{G_last} S_w + k[:, rows of w]^T (e^{G_last - G} v_new)
+//   1.  partial Y_w = k[:, rows of w] S_w and (q S)_w for all 64 tokens     -> LDS
+//   2a. wave w: Y = sum of the partials and r = beta v - beta e^G Y for token tiles 0..w, and
+//       v_new of token tile w = sum_jb T[w][jb] r_jb (T is lower triangular)   -> LDS
+//   2b. every wave reads all of v_new; wave w: o of token tile 3 - w = scale e^G (sum of the
+//       q S partials) + P v_new -> HBM (o tiles 3..0 balance the v_new tiles 0..3: 20 products
+//       per wave); S_w <- e^{G_last} S_w + k[:, rows of w]^T (e^{G_last - G} v_new)
 //
-// so the chain carries 64 + 40 + 32 products per wave per chunk instead of one wave's ~460.  The
-// next chunk is loaded into registers while a chunk is computed.  q is last read in step 1, and
-// T and P (kept as their ten lower 16x16 tiles, in two buffers) are read from the current buffer
-// in step 2, so the next chunk's q, T and P are written into LDS during step 2, and its q, T and
-// P loads for the chunk after issued then; only k (read by step 2's update), v and the gate
-// tables are written between the two barriers that end a chunk.
+// so every wave carries 64 + 20 + 32 products per chunk instead of one wave's ~460 (forming all
+// of v_new in every wave, as an earlier version did, took 64 + 40 + 4..16 + 32 and was 6 %
+// slower at 64 chunks per chain).  The next chunk is loaded into registers while a chunk is
+// computed.  q is last read in step 1, and T and P (kept as their ten lower 16x16 tiles, in two
+// buffers) are read from the current buffer in step 2, so the next chunk's q, T and P are written
+// into LDS during step 2, and its q, T and P loads for the chunk after issued then; only k (read
+// by step 2's update), v and the gate tables are written between the two barriers that end a
+// chunk.
 #pragma once
 
 #include "pf_scan_output.h"
@@ -41,6 +45,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
   __shared__ __attribute__((aligned(16))) float Bs[C], BEG[C], EG[C], EL[C], DL[4];
   __shared__ __attribute__((aligned(16))) floatx4 YP[4 * 4 * 64];   // [wave][token tile][lane]
   __shared__ __attribute__((aligned(16))) floatx4 QP[4 * 4 * 64];
+  __shared__ __attribute__((aligned(16))) floatx4 VX[4 * 64];      // v_new, [token tile][lane]
 
   constexpr int NS = DV / 16;
   const int bh = blockIdx.x / NS, col0 = 16 * (blockIdx.x % NS);
@@ -164,51 +169,51 @@ void scan_split_f32_kernel(ScanOutArgs a) {
     }
     const float* ts = tsb[ch & 1];
     const float* ps = psb[ch & 1];
-    // ---- 2. r, v_new = T r for all tokens; o for tokens 16w ..; the update of rows 32w .. ----
+    // ---- 2a. wave w: r for token tiles 0..w, v_new tile w = sum_jb T[w][jb] r_jb -> VX ----
+    {
+      floatx4 V = zero4();
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        if (jb <= w) {
+          floatx4 Y = YP[jb * 64 + lane];
+#pragma unroll
+          for (int w2 = 1; w2 < 4; ++w2) Y += YP[(w2 * 4 + jb) * 64 + lane];
+          floatx4 R;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int t = 16 * jb + 4 * g + ii;
+            R[ii] = Bs[t] * vs[t * VP + c] - BEG[t] * Y[ii];
+          }
+          const floatx4 ta = *reinterpret_cast<const floatx4*>(ts + score_tile_index(w, jb) * TT + c * TR + 4 * g);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) V = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[ii], R[ii], V, 0, 0, 0);
+        }
+      }
+      VX[w * 64 + lane] = V;
+    }
+    lds_barrier();
+    // ---- 2b. every wave: all of v_new; o for token tile 3 - w; the update of rows 32w .. ----
     floatx4 VN[4];
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      floatx4 Y = YP[ib * 64 + lane];
-#pragma unroll
-      for (int w2 = 1; w2 < 4; ++w2) Y += YP[(w2 * 4 + ib) * 64 + lane];
-      floatx4 R;
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int t = 16 * ib + 4 * g + ii;
-        R[ii] = Bs[t] * vs[t * VP + c] - BEG[t] * Y[ii];
-      }
-      VN[ib] = R;                                      // r until the T products below
-    }
+    for (int ib = 0; ib < 4; ++ib) VN[ib] = VX[ib * 64 + lane];
     {
-      floatx4 V[4];
+      const int ot = 3 - w;                            // o tiles 3..0 balance v_new tiles 0..3
+      floatx4 O = QP[ot * 64 + lane];
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
-        floatx4 acc = zero4();
+      for (int w2 = 1; w2 < 4; ++w2) O += QP[(w2 * 4 + ot) * 64 + lane];
 #pragma unroll
-        for (int jb = 0; jb <= ib; ++jb) {
-          const floatx4 ta = *reinterpret_cast<const floatx4*>(ts + score_tile_index(ib, jb) * TT + c * TR + 4 * g);
+      for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[16 * ot + 4 * g + ii];
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[ii], VN[jb][ii], acc, 0, 0, 0);
+      for (int jb = 0; jb < 4; ++jb) {
+        if (jb <= ot) {
+          const floatx4 pa = *reinterpret_cast<const floatx4*>(ps + score_tile_index(ot, jb) * TT + c * TR + 4 * g);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) O = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ii], VN[jb][ii], O, 0, 0, 0);
         }
-        V[ib] = acc;
-      }
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib) VN[ib] = V[ib];
-    }
-    {
-      floatx4 O = QP[w * 64 + lane];
-#pragma unroll
-      for (int w2 = 1; w2 < 4; ++w2) O += QP[(w2 * 4 + w) * 64 + lane];
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[16 * w + 4 * g + ii];
-      for (int jb = 0; jb <= w; ++jb) {
-        const floatx4 pa = *reinterpret_cast<const floatx4*>(ps + score_tile_index(w, jb) * TT + c * TR + 4 * g);
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) O = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ii], VN[jb][ii], O, 0, 0, 0);
       }
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
-        __builtin_nontemporal_store(O[ii], a.o + ((size_t)bh * Tlen + (size_t)ch * C + 16 * w + 4 * g + ii) * DV + col0 + c);
+        __builtin_nontemporal_store(O[ii], a.o + ((size_t)bh * Tlen + (size_t)ch * C + 16 * ot + 4 * g + ii) * DV + col0 + c);
     }
     {
       const float dl = DL[0];
