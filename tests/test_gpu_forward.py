@@ -239,3 +239,20 @@ def test_gdn_linear_in_v_config2():
     o2, h2 = _run(inp2)
     assert np.array_equal(o2, 2 * o1), max_abs(o2, 2 * o1)
     assert np.array_equal(h2, 2 * h1), max_abs(h2, 2 * h1)
+
+
+@pytest.mark.parametrize("dtype,B,H,T", [(torch.bfloat16, 2, 4, 512), (torch.float32, 1, 4, 512),
+                                         (torch.float32, 4, 16, 1024)])
+def test_gdn_without_final_state(dtype, B, H, T):
+    """output_final_state=False passes a NULL final-state pointer: no state is written, None is
+    returned, and o is bit-identical to the call that also writes the state (the fp32 cases run
+    the split scan and, at 512 slices, the generic one)."""
+    announce(f"GDN {dtype} without final state B{B} H{H} T{T}")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=dtype, seed=11, h0_std=0.02)
+    d = {n: (None if t is None else t.to(DEV)) for n, t in inp.items()}
+    o1, h1 = gdn_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"])
+    o2, h2 = gdn_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"],
+                               output_final_state=False)
+    torch.cuda.synchronize()
+    assert h2 is None and h1 is not None
+    assert torch.equal(o1, o2)

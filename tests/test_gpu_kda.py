@@ -142,3 +142,17 @@ def test_kda_fp32_strong_decay_and_chunk_128():
     _check_fp32("KDA fp32 B1 H2 T512 strong decay C128", o128.cpu().numpy(), h128.cpu().numpy(),
                 o_ref, h_ref)
     assert torch.equal(o128, o64) and torch.equal(h128, h64)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_kda_without_final_state(dtype):
+    """output_final_state=False: no state is written, None is returned, o is bit-identical."""
+    announce(f"KDA {dtype} without final state B1 H4 T512")
+    inp = make_delta_inputs(1, 4, 512, kind="kda", dtype=dtype, seed=13, h0_std=0.02)
+    d = {n: (None if t is None else t.to(DEV)) for n, t in inp.items()}
+    o1, h1 = kda_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"])
+    o2, h2 = kda_chunk_forward(d["q"], d["k"], d["v"], d["beta"], d["g"], h0=d["h0"],
+                               output_final_state=False)
+    torch.cuda.synchronize()
+    assert h2 is None and h1 is not None
+    assert torch.equal(o1, o2)
