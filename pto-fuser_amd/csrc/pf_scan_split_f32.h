@@ -16,11 +16,10 @@
 // so every wave carries 64 + 20 + 32 products per chunk instead of one wave's ~460 (forming all
 // of v_new in every wave, as an earlier version did, took 64 + 40 + 4..16 + 32 and was 6 %
 // slower at 64 chunks per chain).  The next chunk is loaded into registers while a chunk is
-// computed.  q is last read in step 1, and T and P (kept as their ten lower 16x16 tiles, in two
-// buffers) are read from the current buffer in step 2, so the next chunk's q, T and P are written
-// into LDS during step 2, and its q, T and P loads for the chunk after issued then; only k (read
-// by step 2's update), v and the gate tables are written between the two barriers that end a
-// chunk.
+// computed and written into LDS where its last reader is done: each wave's own slice of k and q
+// (the only columns it reads) after its own last read, T, P and the gate tables (two buffers:
+// T and P as their ten lower 16x16 tiles) after the barrier that ends step 1, v after the one
+// that ends step 2a.  Three barriers per chunk, and no copy section between them.
 #pragma once
 
 #include "pf_scan_output.h"
@@ -42,7 +41,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
   __shared__ __attribute__((aligned(16))) float tsb[2][TB];
   __shared__ __attribute__((aligned(16))) float psb[2][TB];
   __shared__ __attribute__((aligned(16))) float vs[C * VP];
-  __shared__ __attribute__((aligned(16))) float Bs[C], BEG[C], EG[C], EL[C], DL[4];
+  __shared__ __attribute__((aligned(16))) float Bs[2][C], BEG[2][C], EG[2][C], EL[2][C], DL[2][4];
   __shared__ __attribute__((aligned(16))) floatx4 YP[4 * 4 * 64];   // [wave][token tile][lane]
   __shared__ __attribute__((aligned(16))) floatx4 QP[4 * 4 * 64];
   __shared__ __attribute__((aligned(16))) floatx4 VX[4 * 64];      // v_new, [token tile][lane]
@@ -60,71 +59,68 @@ void scan_split_f32_kernel(ScanOutArgs a) {
   const float* pb = static_cast<const float*>(a.P) + (size_t)bh * NC * C * C;
   const float oscale = *a.scale;
 
-  // ---- one chunk: global -> registers -> LDS ----
-  floatx4 rk[NK], rq[NK], rt[NT], rp[NT], rv;
+  // ---- chunk data: global -> registers -> LDS.  Wave w reads only columns 32w .. 32w+31 of the
+  //      k and q rows (its state rows), so it loads and writes that slice itself and refills it
+  //      after its own last read, with no workgroup barrier; T, P and the gate tables (two
+  //      buffers) are written after B1, v after B2 (its last read is in step 2a) ----
+  floatx4 rk[8], rq[8], rt[NT], rp[NT], rv;
   float rg = 0.f, rb = 0.f;
+  static_assert(NK == 8, "64 rows x 32 columns of k (or q) per wave: eight float4 per lane");
+  auto kq_lds = [&](int i) { const int u = lane + 64 * i; return (u >> 3) * KP + 32 * w + 4 * (u & 7); };
+  auto kq_mem = [&](int i) { const int u = lane + 64 * i; return (size_t)(u >> 3) * DK + 32 * w + 4 * (u & 7); };
+  auto load_k = [&](int ch) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rk[i] = *reinterpret_cast<const floatx4*>(kb + (size_t)ch * C * DK + kq_mem(i));
+  };
+  auto load_q = [&](int ch) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rq[i] = *reinterpret_cast<const floatx4*>(qb + (size_t)ch * C * DK + kq_mem(i));
+  };
+  auto store_k = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<floatx4*>(ks + kq_lds(i)) = rk[i];
+  };
+  auto store_q = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<floatx4*>(qs + kq_lds(i)) = rq[i];
+  };
   // thread tid holds T / P rows 16 i + tid / 16, columns 4 (tid % 16) .. : tile (i, (tid % 16) / 4)
   const int t_row = tid >> 4, t_jb = (tid & 15) >> 2, t_col = 4 * (tid & 3);
-  auto load_qtp = [&](int ch) {
-    const size_t t0 = (size_t)ch * C;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
-      rq[i] = *reinterpret_cast<const floatx4*>(qb + (t0 + row) * DK + 4 * q4);
-    }
+  auto load_tpg = [&](int ch) {
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
       const int u = tid + 256 * i, row = u >> 4, q4 = u & 15;
       rt[i] = *reinterpret_cast<const floatx4*>(tb + ((size_t)ch * C + row) * C + 4 * q4);
       rp[i] = *reinterpret_cast<const floatx4*>(pb + ((size_t)ch * C + row) * C + 4 * q4);
     }
+    // every thread loads (threads 64.. repeat the first wave's tokens): no branch around a load;
+    // G is the stage-1 workspace's cumsum, always present for this kernel
+    rg = a.G[(size_t)bh * Tlen + (size_t)ch * C + (tid & (C - 1))];
+    rb = a.beta[(size_t)bh * Tlen + (size_t)ch * C + (tid & (C - 1))];
   };
-  auto store_qtp = [&](int ch) {
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
-      *reinterpret_cast<floatx4*>(qs + row * KP + 4 * q4) = rq[i];
-    }
-    float* tsd = tsb[ch & 1];
-    float* psd = psb[ch & 1];
+  auto store_tpg = [&](int ch) {
+    const int b = ch & 1;
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
       if (t_jb <= i) {
         const int off = score_tile_index(i, t_jb) * TT + t_row * TR + t_col;
-        *reinterpret_cast<floatx4*>(tsd + off) = rt[i];
-        *reinterpret_cast<floatx4*>(psd + off) = rp[i];
+        *reinterpret_cast<floatx4*>(tsb[b] + off) = rt[i];
+        *reinterpret_cast<floatx4*>(psb[b] + off) = rp[i];
       }
     }
-  };
-  auto load = [&](int ch) {
-    const size_t t0 = (size_t)ch * C;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
-      rk[i] = *reinterpret_cast<const floatx4*>(kb + (t0 + row) * DK + 4 * q4);
-    }
-    rv = *reinterpret_cast<const floatx4*>(vb + (t0 + (tid >> 2)) * DV + col0 + 4 * (tid & 3));
-    if (tid < C) {
-      rg = a.G ? a.G[(size_t)bh * Tlen + t0 + tid] : 0.f;
-      rb = a.beta[(size_t)bh * Tlen + t0 + tid];
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const int u = tid + 256 * i, row = u >> 5, q4 = u & 31;
-      *reinterpret_cast<floatx4*>(ks + row * KP + 4 * q4) = rk[i];
-    }
-    *reinterpret_cast<floatx4*>(vs + (tid >> 2) * VP + 4 * (tid & 3)) = rv;
     if (w == 0) {                                     // lane = token
       const float gl = __shfl(rg, C - 1);
-      Bs[lane] = rb;
-      BEG[lane] = rb * __expf(rg);
-      EG[lane] = oscale * __expf(rg);
-      EL[lane] = __expf(gl - rg);
-      if (lane == 0) DL[0] = __expf(gl);
+      Bs[b][lane] = rb;
+      BEG[b][lane] = rb * __expf(rg);
+      EG[b][lane] = oscale * __expf(rg);
+      EL[b][lane] = __expf(gl - rg);
+      if (lane == 0) DL[b][0] = __expf(gl);
     }
   };
+  auto load_v = [&](int ch) {
+    rv = *reinterpret_cast<const floatx4*>(vb + ((size_t)ch * C + (tid >> 2)) * DV + col0 + 4 * (tid & 3));
+  };
+  auto store_v = [&]() { *reinterpret_cast<floatx4*>(vs + (tid >> 2) * VP + 4 * (tid & 3)) = rv; };
 
   floatx4 S[2];                                       // rows 32w + 16r + 4g + ii, column col0 + c
 #pragma unroll
@@ -133,17 +129,28 @@ void scan_split_f32_kernel(ScanOutArgs a) {
     for (int ii = 0; ii < 4; ++ii)
       S[r][ii] = a.h0 ? a.h0[((size_t)bh * DK + 32 * w + 16 * r + 4 * g + ii) * DV + col0 + c] : 0.f;
 
-  load(0);
-  load_qtp(0);
-  store();
-  store_qtp(0);
+  load_k(0);
+  load_q(0);
+  load_tpg(0);
+  load_v(0);
+  store_k();
+  store_q();
+  store_tpg(0);
+  store_v();
   lds_barrier();
-  if (NC > 1) {
-    load(1);
-    load_qtp(1);
-  }
+  load_k(min(1, NC - 1));
+  load_q(min(1, NC - 1));
+  load_tpg(min(1, NC - 1));
+  load_v(min(1, NC - 1));
 
+  // Past the end the loads repeat the last chunk and the copies write what no one reads again
+  // (a wave's own slices after its last read, the other T / P / gate buffer, v after its last
+  // read): the loop body is straight-line code, so the compiler's wait counts stay exact and a
+  // copy waits only for its own loads, issued a chunk earlier.
+  const int last = NC - 1;
   for (int ch = 0; ch < NC; ++ch) {
+    const int cb = ch & 1;
+    const int nx2 = min(ch + 2, last);
     // ---- 1. partial products over this wave's 32 state rows ----
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
@@ -161,14 +168,13 @@ void scan_split_f32_kernel(ScanOutArgs a) {
       YP[(w * 4 + ib) * 64 + lane] = y;
       QP[(w * 4 + ib) * 64 + lane] = qy;
     }
-    lds_barrier();
-    // q of this chunk is read: the next chunk's q, and its T and P into the other buffer
-    if (ch + 1 < NC) {
-      store_qtp(ch + 1);
-      if (ch + 2 < NC) load_qtp(ch + 2);
-    }
-    const float* ts = tsb[ch & 1];
-    const float* ps = psb[ch & 1];
+    store_q();                                         // this wave's q slice is read
+    load_q(nx2);
+    lds_barrier();                                     // B1: partials written
+    store_tpg(ch + 1);                                 // the other T / P / gate buffer is free
+    load_tpg(nx2);
+    const float* ts = tsb[cb];
+    const float* ps = psb[cb];
     // ---- 2a. wave w: r for token tiles 0..w, v_new tile w = sum_jb T[w][jb] r_jb -> VX ----
     {
       floatx4 V = zero4();
@@ -182,7 +188,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
             const int t = 16 * jb + 4 * g + ii;
-            R[ii] = Bs[t] * vs[t * VP + c] - BEG[t] * Y[ii];
+            R[ii] = Bs[cb][t] * vs[t * VP + c] - BEG[cb][t] * Y[ii];
           }
           const floatx4 ta = *reinterpret_cast<const floatx4*>(ts + score_tile_index(w, jb) * TT + c * TR + 4 * g);
 #pragma unroll
@@ -191,7 +197,9 @@ void scan_split_f32_kernel(ScanOutArgs a) {
       }
       VX[w * 64 + lane] = V;
     }
-    lds_barrier();
+    lds_barrier();                                     // B2: v_new written, v read
+    store_v();
+    load_v(nx2);
     // ---- 2b. every wave: all of v_new; o for token tile 3 - w; the update of rows 32w .. ----
     floatx4 VN[4];
 #pragma unroll
@@ -202,7 +210,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
 #pragma unroll
       for (int w2 = 1; w2 < 4; ++w2) O += QP[(w2 * 4 + ot) * 64 + lane];
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[16 * ot + 4 * g + ii];
+      for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[cb][16 * ot + 4 * g + ii];
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         if (jb <= ot) {
@@ -216,7 +224,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
         __builtin_nontemporal_store(O[ii], a.o + ((size_t)bh * Tlen + (size_t)ch * C + 16 * ot + 4 * g + ii) * DV + col0 + c);
     }
     {
-      const float dl = DL[0];
+      const float dl = DL[cb][0];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         floatx4 acc = S[r] * dl;
@@ -225,17 +233,14 @@ void scan_split_f32_kernel(ScanOutArgs a) {
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
             const int t = 16 * jb + 4 * g + ii;
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[t * KP + 32 * w + 16 * r + c], EL[t] * VN[jb][ii], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[t * KP + 32 * w + 16 * r + c], EL[cb][t] * VN[jb][ii], acc, 0, 0, 0);
           }
         S[r] = acc;
       }
     }
-    lds_barrier();                                     // the chunk's image and partials are read
-    if (ch + 1 < NC) {
-      store();
-      lds_barrier();
-      if (ch + 2 < NC) load(ch + 2);
-    }
+    store_k();                                         // this wave's k slice is read
+    load_k(nx2);
+    lds_barrier();                                     // B3: the chunk's exchanges are read
   }
   if (a.h_final) {
 #pragma unroll
