@@ -11,7 +11,7 @@
 #include "pf_chunk_local.h"
 #include "pf_status.h"
 #include "pf_workspace.h"
-#include "pf_scan_output.h"
+#include "pf_scan_args.h"
 #include "pf_scan_split.h"
 #include "pf_scan_split_f32.h"
 
@@ -104,7 +104,7 @@ template <typename E>
 void scan_output_launch(const void* q, const void* k, const void* v, const float* beta,
                        const float* h0, float* o, float* h_final, int BH, int NC,
                        char* base, hipStream_t stream) {
-  constexpr int C = 64, DK = 128, DV = 128, NWC = 2;
+  constexpr int C = 64, DK = 128, DV = 128;
   const size_t M = (size_t)BH * NC;
   const GdnLayout lay(M, C, std::is_same<E, bf16>::value ? PF_DTYPE_BF16 : PF_DTYPE_F32);
   pf::ScanOutArgs a{};
@@ -131,15 +131,10 @@ void scan_output_launch(const void* q, const void* k, const void* v, const float
     else
       pf::scan_split_kernel<C, DK, DV, 2, kSplitLoaderWaves>
           <<<dim3((unsigned)(BH * (DV / 32))), dim3(64 * (4 + kSplitLoaderWaves)), 0, stream>>>(a);
-  } else if ((size_t)BH * (DV / 16) <= (size_t)device_cu_count()) {
-    // fp32, at most one (chain, 16-column) slice per CU: every chunk split over four waves
-    // (pf_scan_split_f32.h); beyond that the two-wave kernel's 32-column slices fill the CUs better
-    pf::scan_split_f32_kernel<C, DK, DV><<<dim3((unsigned)(BH * (DV / 16))), dim3(256), 0, stream>>>(a);
   } else {
-    // fp32: transposed tiles staged by the loader; one LDS buffer (the images are 143 KB)
-    const unsigned grid = (unsigned)(BH * (DV / (16 * NWC)));
-    pf::scan_output_kernel<E, C, DK, DV, NWC, 1>
-        <<<dim3(grid), dim3(64 * (NWC + pf::kLoaderWaves)), 0, stream>>>(a);
+    // fp32: one workgroup per (chain, 16-column slice), every chunk split over four waves
+    // (pf_scan_split_f32.h)
+    pf::scan_split_f32_kernel<C, DK, DV><<<dim3((unsigned)(BH * (DV / 16))), dim3(256), 0, stream>>>(a);
   }
 }
 

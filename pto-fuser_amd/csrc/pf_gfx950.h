@@ -3,7 +3,7 @@
 // bf16 MFMA, and the renormalisation threshold of the deferred state decay.
 #pragma once
 
-#include "pf_scan_output.h"
+#include "pf_device.h"
 
 namespace pf {
 

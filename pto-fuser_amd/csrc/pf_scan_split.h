@@ -53,6 +53,7 @@
 #include <type_traits>
 
 #include "pf_gfx950.h"
+#include "pf_scan_args.h"
 
 namespace pf {
 

@@ -1,6 +1,6 @@
-// Stage 2 for fp32 operands with every chunk's work split over four waves: the state scan fused
-// with the output, for short sequences and few chains, where one wave walking a chain's whole
-// chunk (pf_scan_output.h) leaves the chain's latency as the forward's time.
+// Stage 2 for fp32 operands: the state scan fused with the output, every chunk's work split over
+// four waves so that the chain's latency (the forward's time at few chains) is a quarter of one
+// wave walking the whole chunk.
 //
 // Workgroup = one chain bh x one 16-column slice (grid BH * DV / 16), four waves.  Wave w owns
 // state rows 32w .. 32w+31 (fp32, MFMA D layout, in registers for the whole chain).  Per chunk
@@ -22,7 +22,7 @@
 // that ends step 2a.  Three barriers per chunk, and no copy section between them.
 #pragma once
 
-#include "pf_scan_output.h"
+#include "pf_scan_args.h"
 
 namespace pf {
 

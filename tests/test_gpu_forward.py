@@ -94,7 +94,7 @@ def test_deltanet_fp32_config1():
            bf16=False)
 
 
-@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 256), (1, 8, 1024)])
+@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 256), (1, 8, 1024), (4, 16, 1024)])
 def test_gdn_fp32_with_h0(B, H, T):
     announce(f"GDN fp32 B{B} H{H} T{T} h0")
     inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.float32, seed=B * 100 + H, h0_std=0.02)
@@ -245,8 +245,8 @@ def test_gdn_linear_in_v_config2():
                                          (torch.float32, 4, 16, 1024)])
 def test_gdn_without_final_state(dtype, B, H, T):
     """output_final_state=False passes a NULL final-state pointer: no state is written, None is
-    returned, and o is bit-identical to the call that also writes the state (the fp32 cases run
-    the split scan and, at 512 slices, the generic one)."""
+    returned, and o is bit-identical to the call that also writes the state (the fp32 cases at
+    32 and 512 slices: one and two generations of scan workgroups)."""
     announce(f"GDN {dtype} without final state B{B} H{H} T{T}")
     inp = make_delta_inputs(B, H, T, kind="gdn", dtype=dtype, seed=11, h0_std=0.02)
     d = {n: (None if t is None else t.to(DEV)) for n, t in inp.items()}
