@@ -43,8 +43,9 @@
 // loader waves run at the default wave priority: a burst of loads or LDS writes issued at once,
 // or at a raised priority, was measured to stall the compute waves sharing the SIMDs (one phase
 // lost up to 1 000 cycles; q's loads in the first phase beside k's cost 5 % of the kernel).
-// The compute waves store their o rows themselves, one non-temporal 16-byte store per lane and
-// column block.  The loaders also carry the deferred state decay: the compute waves hold
+// The compute waves store their o rows themselves, non-temporal 16-byte stores, two per lane
+// (with 32-column slices the two halves of a token's 128-byte row are swapped between lanes c and
+// c + 8 first, so that every store instruction writes whole lines).  The loaders also carry the deferred state decay: the compute waves hold
 // S~ = S / f with a running factor f folded into the gate tables, and multiply it back only when
 // the loader flags a renormalisation (f below e^-60, or the last chunk, so the final state is
 // exact).
@@ -517,14 +518,37 @@ void scan_split_kernel(ScanOutArgs a) {
         // non-temporal (o is never read here; streaming it past L2 leaves the cache to the k, q
         // and T lines the chain's other column slices read: 7 % of the kernel's time)
         const float egs = s.EGS[tok0 + c];
-        const uint32_t ooff = (uint32_t)(((size_t)ch * C + tok0 + c) * DV + col0 + 4 * g) * 4;
+        if constexpr (NT == 2) {
+          // a token's 32 columns are one 128-byte line: lanes c and c + 8 of a row swap halves
+          // (DPP row rotate by 8) so that each store instruction writes eight whole lines, tokens
+          // 0..7 then 8..15 of the block (two half-line stores reach memory apart when streamed)
+          floatx4 v0, v1;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+          for (int ii = 0; ii < 4; ++ii) {
+            v0[ii] = fmaf(egs, QT[0][ii], OT[0][ii]);
+            v1[ii] = fmaf(egs, QT[1][ii], OT[1][ii]);
+          }
+          const bool hi = c >= 8;
+          floatx4 sa, sb;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const float send = hi ? v0[ii] : v1[ii];
+            const float recv = __int_as_float(__builtin_amdgcn_update_dpp(
+                __float_as_int(send), __float_as_int(send), 0x128, 0xf, 0xf, false));   // row_ror:8
+            sa[ii] = hi ? recv : v0[ii];                 // token c & 7, columns 16 hi + 4g ..
+            sb[ii] = hi ? v1[ii] : recv;                 // token 8 + (c & 7), same columns
+          }
+          const uint32_t col = col0 + (hi ? 16 : 0) + 4 * g;
+          const uint32_t ra = (uint32_t)(((size_t)ch * C + tok0 + (c & 7)) * DV + col) * 4;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sa), ro, ra, 0, kCachePolicyNT);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sb), ro, ra + 8 * DV * 4, 0,
+                                                 kCachePolicyNT);
+        } else {
+          const uint32_t ooff = (uint32_t)(((size_t)ch * C + tok0 + c) * DV + col0 + 4 * g) * 4;
           floatx4 val;
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) val[ii] = fmaf(egs, QT[nt][ii], OT[nt][ii]);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, ooff + 64 * nt, 0,
-                                                 kCachePolicyNT);
+          for (int ii = 0; ii < 4; ++ii) val[ii] = fmaf(egs, QT[0][ii], OT[0][ii]);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, ooff, 0, kCachePolicyNT);
         }
       }
       if (s.DL[1] != 0.f) {
