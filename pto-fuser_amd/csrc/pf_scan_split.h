@@ -43,9 +43,10 @@
 // loader waves run at the default wave priority: a burst of loads or LDS writes issued at once,
 // or at a raised priority, was measured to stall the compute waves sharing the SIMDs (one phase
 // lost up to 1 000 cycles; q's loads in the first phase beside k's cost 5 % of the kernel).
-// The compute waves store their o rows themselves, non-temporal 16-byte stores, two per lane
-// (with 32-column slices the two halves of a token's 128-byte row are swapped between lanes c and
-// c + 8 first, so that every store instruction writes whole lines).  The loaders also carry the deferred state decay: the compute waves hold
+// The compute waves store their o rows themselves, 16-byte stores: with 32-column slices two per
+// lane, non-temporal, after lanes c and c + 8 swap the halves of a token's 128-byte row so that
+// every store instruction writes whole lines; with 16-column slices one per lane, through the
+// cache (the line's other half comes from the neighbouring slice's workgroup).  The loaders also carry the deferred state decay: the compute waves hold
 // S~ = S / f with a running factor f folded into the gate tables, and multiply it back only when
 // the loader flags a renormalisation (f below e^-60, or the last chunk, so the final state is
 // exact).
@@ -544,11 +545,15 @@ void scan_split_kernel(ScanOutArgs a) {
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sb), ro, ra + 8 * DV * 4, 0,
                                                  kCachePolicyNT);
         } else {
+          // 16-column slices: the other half of each 128-byte line comes from the neighbouring
+          // slice's workgroup (same XCD), so o is stored through the cache, where the halves
+          // meet before write-back (streamed, they reached memory apart: o written 12 % over its
+          // size, at the same speed)
           const uint32_t ooff = (uint32_t)(((size_t)ch * C + tok0 + c) * DV + col0 + 4 * g) * 4;
           floatx4 val;
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) val[ii] = fmaf(egs, QT[0][ii], OT[0][ii]);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, ooff, 0, kCachePolicyNT);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ro, ooff, 0, 0);
         }
       }
       if (s.DL[1] != 0.f) {
