@@ -94,7 +94,8 @@ def test_deltanet_fp32_config1():
            bf16=False)
 
 
-@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (2, 3, 256), (1, 8, 1024), (4, 16, 1024)])
+@pytest.mark.parametrize("B,H,T", [(1, 2, 64), (1, 2, 128), (2, 1, 192), (2, 3, 256), (1, 8, 1024),
+                                   (4, 16, 1024)])
 def test_gdn_fp32_with_h0(B, H, T):
     announce(f"GDN fp32 B{B} H{H} T{T} h0")
     inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.float32, seed=B * 100 + H, h0_std=0.02)
