@@ -67,6 +67,9 @@ void* pf_gdn_setup(int B, int H, int T, int C, int DK, int DV, int dtype);
  * empty handle (allocates nothing); pf_gdn_reserve grows it to the shape's size (PF_OK, PF_ERR_ARG
  * for an unsupported shape, PF_ERR_ALLOC).  A reserve that does not grow allocates nothing and is
  * safe under HIP graph capture; one that grows waits for the device and must run outside it.
+ * Growing frees the old buffer: a HIP graph captured on the handle before a growth still
+ * addresses it and must be captured again.  The fp32 layout of a shape holds its bf16 layout, so
+ * a handle reserved for the fp32 size serves both dtypes of that shape without growing.
  * pf_gdn_setup(shape) == pf_gdn_create() + pf_gdn_reserve(shape); pf_gdn_teardown frees either. */
 void* pf_gdn_create(void);
 int pf_gdn_reserve(void* ws, int B, int H, int T, int C, int DK, int DV, int dtype);
@@ -117,8 +120,8 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
  *   q, k [B,H,T,DK] and v [B,H,T,DV] of `dtype`; beta [B,H,T] fp32; g [B,H,T,DK] fp32
  *   (per-token, per-channel log decay, summed within each chunk of C tokens by the kernel);
  *   h0 [B,H,DK,DV] fp32 or NULL; o [B,H,T,DV] fp32 (scaled by `scale`); h_final [B,H,DK,DV]
- *   fp32 or NULL.  Supported: dtype PF_DTYPE_BF16 (bf16 MFMA, T >= 128) or PF_DTYPE_F32 (fp32
- *   operands and fp32 MFMA throughout, T >= 64), C = 64 or 128 (run as 64-token chunks),
+ *   fp32 or NULL.  Supported: dtype PF_DTYPE_BF16 (bf16 MFMA) or PF_DTYPE_F32 (fp32
+ *   operands and fp32 MFMA throughout), C = 64 or 128 (run as 64-token chunks),
  *   DK = DV = 128, T % C == 0, T <= 4 194 304.  The workspace holds the stage-1 images in the
  *   operand type.
  * ------------------------------------------------------------------------------------------ */

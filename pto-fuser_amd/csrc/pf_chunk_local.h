@@ -291,11 +291,20 @@ __device__ __forceinline__ void score_wave(const ChunkLocalArgs& a, const E* ks,
 }
 
 // One workgroup per chunk; eight workgroups fit a CU for bf16 without P (at most 64 VGPRs and
-// 17.9 KB of LDS each; four with P or fp32, which the LDS limits), so the HBM latency of one
-// chunk's loads overlaps the other workgroups' products and inverse.  At the headline's 16 chunks
-// per CU that is two generations of workgroups instead of three.
+// 17.9 KB of LDS each), so the HBM latency of one chunk's loads overlaps the other workgroups'
+// products and inverse.  At the headline's 16 chunks per CU that is two generations of workgroups
+// instead of three.  The fp32 tiles' LDS allows four workgroups per CU without P, two with it;
+// the register target follows, so the compiler does not trade registers for residency the LDS
+// cannot give.
+template <typename E, bool DO_P>
+struct ChunkLocalWaves {
+  static constexpr int value = (sizeof(E) == 2 && !DO_P) ? 8 : DO_P ? 2 : 4;
+};
+
 template <typename E, typename TO, int C, int DK, bool DO_P, bool DO_INV>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void chunk_local_kernel(ChunkLocalArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ChunkLocalWaves<E, DO_P>::value,
+                                                                      ChunkLocalWaves<E, DO_P>::value)))
+void chunk_local_kernel(ChunkLocalArgs a) {
   static_assert(C == 64, "the chunk-local kernel is written for 64-token chunks");
   static_assert(DK % Mfma<E>::KB == 0, "head dim must be a multiple of the MFMA K block");
   constexpr int PE = 16 / sizeof(E);

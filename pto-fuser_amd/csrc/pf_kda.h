@@ -430,7 +430,9 @@ void kda_scan_kernel(KdaScanArgs a) {
     };
     // Same schedule as the GDN scan kernel: step j (between barriers j and j+1) issues the loads
     // of chunk j+2, writes out the o of chunk j-2, stores chunk j into buffer j & 1; three
-    // register sets rotate; NC >= 2.
+    // register sets rotate.  The compute waves pass NC + 1 barriers (one before the first chunk,
+    // one after each); so do the loaders: barrier 1, the steps 1 .. NC-1, barrier NC + 1.  With
+    // one chunk there is no step and no o two chunks back.
     const int last = NC - 1;
     Regs r0, r1, r2;
     auto step = [&](Regs& ld, Regs& sd, int j, bool with_o) {
@@ -444,16 +446,18 @@ void kda_scan_kernel(KdaScanArgs a) {
     load_chunk(r2, min(2, last));
     store_chunk(st[0], r0);
     lds_barrier();                                       // barrier 1
-    step(r0, r1, 1, false);
-    int j = 2;
-    for (; j + 2 < NC; j += 3) {
-      step(r1, r2, j, true);
-      step(r2, r0, j + 1, true);
-      step(r0, r1, j + 2, true);
+    if (NC > 1) {
+      step(r0, r1, 1, false);
+      int j = 2;
+      for (; j + 2 < NC; j += 3) {
+        step(r1, r2, j, true);
+        step(r2, r0, j + 1, true);
+        step(r0, r1, j + 2, true);
+      }
+      if (j < NC) step(r1, r2, j, true);
+      if (j + 1 < NC) step(r2, r0, j + 1, true);
+      store_o(ost[NC & 1], NC - 2);
     }
-    if (j < NC) step(r1, r2, j, true);
-    if (j + 1 < NC) step(r2, r0, j + 1, true);
-    store_o(ost[NC & 1], NC - 2);
     lds_barrier();                                       // barrier NC + 1
     store_o(ost[(NC - 1) & 1], NC - 1);
   } else {

@@ -34,8 +34,7 @@ struct KdaLayout {
   }
 };
 
-// bf16 operands with at least two chunks per chain (the bf16 scan kernel's loader pipeline is
-// written for NC >= 2), or fp32 operands (the fp32 kernels of pf_kda_f32.h); dk = dv = 128.
+// bf16 operands (pf_kda.h) or fp32 operands (the fp32 kernels of pf_kda_f32.h); dk = dv = 128.
 // 64-token chunks in the kernels; a caller's chunk size of 128 runs them over T / 64 chunks (the
 // chunked forward's result does not depend on the chunk size), with T a multiple of 128.
 constexpr int kChunk = 64;
@@ -43,7 +42,7 @@ constexpr int kChunk = 64;
 bool kda_shape_ok(int B, int H, int T, int C, int DK, int DV, int dtype) {
   return B > 0 && H > 0 && T > 0 && T <= pf::kMaxChainTokens && (C == 64 || C == 128) &&
          DK == 128 && DV == 128 && T % C == 0 &&
-         ((dtype == PF_DTYPE_BF16 && T / kChunk >= 2) || dtype == PF_DTYPE_F32);
+         (dtype == PF_DTYPE_BF16 || dtype == PF_DTYPE_F32);
 }
 
 }  // namespace

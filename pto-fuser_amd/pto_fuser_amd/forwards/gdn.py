@@ -21,15 +21,15 @@ kernels; this Program exists for the compile stack.
 """
 from __future__ import annotations
 
-from typing import Dict, List, Tuple
+from typing import Dict, List
 
 import torch
 
-from ..ir import EinsumNode, Program
+from ..ir import Program
 from ._builder import ProgramBuilder
 
 __all__ = ["make_gdn_inputs", "prepare_gdn_bindings", "build_gdn_program",
-           "gdn_contraction_stages", "GDN_PROGRAM_INPUTS"]
+           "GDN_PROGRAM_INPUTS"]
 
 GDN_PROGRAM_INPUTS = ["qF", "kF", "vF", "coefA", "coef_kb", "coef_vb", "coef_qg", "coef_o",
                       "coef_vcs", "coef_S", "g_native", "beta_native", "beta_native_ones"]
@@ -148,34 +148,3 @@ def build_gdn_program(B, H, nc, C, D, scale, work=torch.bfloat16) -> Program:
     p.op("o", "reshape", "o_s", shape=[B, H, nc, C, D])
     return p.program(GDN_PROGRAM_INPUTS, ["o"])
 
-
-def _single_einsum(eq: str) -> Program:
-    lhs, out = eq.split("->")
-    a, b = (s.strip() for s in lhs.split(","))
-    return Program(nodes=[EinsumNode(eq, [a, b], out.strip(), out_dtype=torch.bfloat16)],
-                   inputs=[a, b], outputs=[out.strip()])
-
-
-def gdn_contraction_stages(B: int = 2, nc: int = 4, H: int = 16, C: int = 64, D: int = 128,
-                           device="cuda:0", dtype=torch.bfloat16, seed: int = 0
-                           ) -> List[Tuple[str, Program, Dict[str, torch.Tensor]]]:
-    """The four GDN contractions on the head-interleaved token layout as single-einsum
-    Programs with random operands (src/pto_fuser/forwards/gdn.py:36-70): kkt
-    ``bihd,bjhd->bihj``, wy ``bihj,bjhd->bihd``, chunk_h ``bvhd,bvhe->bhde``, chunk_o
-    ``bvhd,bhde->bvhe`` with the leading batch B·nc."""
-    Bn = B * nc
-    gen = torch.Generator().manual_seed(seed)
-
-    def rand(*shape):
-        return torch.randn(*shape, generator=gen).to(dtype).to(device)
-
-    return [
-        ("kkt", _single_einsum("bihd,bjhd->bihj"),
-         {"bihd": rand(Bn, C, H, D), "bjhd": rand(Bn, C, H, D)}),
-        ("wy_fast", _single_einsum("bihj,bjhd->bihd"),
-         {"bihj": rand(Bn, C, H, C), "bjhd": rand(Bn, C, H, D)}),
-        ("chunk_h", _single_einsum("bvhd,bvhe->bhde"),
-         {"bvhd": rand(Bn, C, H, D), "bvhe": rand(Bn, C, H, D)}),
-        ("chunk_o", _single_einsum("bvhd,bhde->bvhe"),
-         {"bvhd": rand(Bn, C, H, D), "bhde": rand(Bn, H, D, D)}),
-    ]

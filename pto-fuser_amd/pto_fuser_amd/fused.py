@@ -442,7 +442,7 @@ def default_fused_registry() -> FusedKernelRegistry:
             in_dtypes=[_BF, _BF, _BF, _F32, _F32], out_names=["o"], out_dtype=_F32,
             notes="whole KDA forward: q/k/v [M,C,D] (bf16, or fp32 end to end), per-channel "
                   "cumulative gate g_native [M,C,D] and beta [M,C] fp32 -> o [B,H,nc,C,D] fp32; "
-                  "C = 64 or 128, D = 128, bf16 T >= 128")))
+                  "C = 64 or 128, D = 128")))
     return reg
 
 

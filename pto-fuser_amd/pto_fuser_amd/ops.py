@@ -372,7 +372,7 @@ def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
     g [B,H,T,DK] float32 (the per-token, per-channel log decay, summed within chunks by the
     kernel); h0 [B,H,DK,DV] float32 or None.  Returns (o [B,H,T,DV] float32 scaled by ``scale``
     (default DK^-1/2), h_final [B,H,DK,DV] float32 or None).  chunk_size 64 or 128 (both run
-    64-token chunks); bfloat16 needs at least two 64-token chunks per sequence (T >= 128)."""
+    64-token chunks)."""
     if q.dim() != 4:
         raise ValueError(f"q must be [B,H,T,DK], got shape {tuple(q.shape)}")
     B, H, T, DK = q.shape
@@ -385,8 +385,6 @@ def kda_chunk_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: t
         raise ValueError(f"the fused KDA forward takes bfloat16 or float32 operands, got {q.dtype}")
     if T % C:
         raise ValueError(f"T={T} must be a multiple of the chunk size {C}")
-    if q.dtype == torch.bfloat16 and T // 64 < 2:
-        raise ValueError(f"T={T}: bfloat16 operands need at least two chunks of 64 tokens")
     dev = q.device
     if dev.type != "cuda":
         raise ValueError(f"q must be on a HIP device, got {dev}")

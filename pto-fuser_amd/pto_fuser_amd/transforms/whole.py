@@ -12,8 +12,7 @@ they replace every step of a program that computes the forward from the builder'
 A program qualifies when it is the builder's forward (its family's coefficient among the inputs,
 the opaque ``tri_inv_rec_unroll`` solve, the ``o_s`` scale step, output ``o`` only) and its shape
 is one the fused kernels run (C = 64 or 128 — the kernels run 64-token chunks, and a 128-token
-program regroups the same arithmetic — and D = 128; KDA in bf16 also at least two 64-token
-chunks).  The
+program regroups the same arithmetic — and D = 128).  The
 scale is read from the ``o_s`` step, so the fused node computes the same function; the compile
 driver still verifies it against the canonical program before keeping it.
 
@@ -92,11 +91,8 @@ class FuseGdnForward(_WholeForward):
 
 class FuseKdaForward(_WholeForward):
     """KDA (per-channel decay): the program with ``coef_krest`` -> ``kda_forward``; the fused
-    KDA kernels take bf16 operands (at least two 64-token chunks) or fp32 operands."""
+    KDA kernels take bf16 or fp32 operands."""
     name = "fuse-kda-forward"
     summary = "whole KDA program -> kda_forward FusedNode (chunk-local + scan/output kernels)"
     family_input = "coef_krest"
     kernel = "kda_forward"
-
-    def _shape_ok(self) -> bool:
-        return super()._shape_ok() and (self.work == torch.float32 or self.nc * self.C >= 128)

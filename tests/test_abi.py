@@ -80,6 +80,17 @@ def test_workspace_sizing_contract(lib):
     assert not lib.pf_gdn_setup(1, 1, 100, 64, 128, 128, 1)
 
 
+@pytest.mark.parametrize("B,H,T,C", [(1, 1, 64, 64), (4, 16, 4096, 64), (1, 32, 32768, 128),
+                                     (3, 5, 192, 64)])
+def test_fp32_workspace_holds_bf16(lib, B, H, T, C):
+    """A handle reserved for the fp32 layout of a shape serves the bf16 call of that shape
+    without growing (the integration stub reserves it so)."""
+    for fn in (lib.pf_gdn_workspace_bytes, lib.pf_kda_workspace_bytes):
+        f32 = fn(B, H, T, C, 128, 128, _hip.PF_DTYPE_F32)
+        b16 = fn(B, H, T, C, 128, 128, _hip.PF_DTYPE_BF16)
+        assert 0 < b16 <= f32
+
+
 def test_kda_workspace_and_rejects(lib):
     # W, U, QE, KR (bf16 [M,C,128] each) + P (bf16 [M,C,C]) + DEC (fp32 [M,128]), 256-B aligned
     M = 2 * 32 * 128
@@ -92,7 +103,8 @@ def test_kda_workspace_and_rejects(lib):
         + (M1 * 128 * 4 + 255) // 256 * 256
     assert lib.pf_kda_workspace_bytes(1, 1, 8192, 64, 128, 128, _hip.PF_DTYPE_F32) == want32
     assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_F32) > 0     # one chunk
-    assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_BF16) == 0    # bf16: two
+    assert lib.pf_kda_workspace_bytes(1, 1, 64, 64, 128, 128, _hip.PF_DTYPE_BF16) > 0    # bf16 too
+    assert lib.pf_kda_workspace_bytes(1, 1, 96, 64, 128, 128, _hip.PF_DTYPE_BF16) == 0   # T % C
     assert not lib.pf_kda_setup(1, 1, 100, 64, 128, 128, 1)
     assert lib.pf_kda_workspace_bytes(1, 1, 1 << 22, 64, 128, 128, 1) > 0
     assert lib.pf_kda_workspace_bytes(1, 1, (1 << 22) + 64, 64, 128, 128, 1) == 0
@@ -103,7 +115,9 @@ def test_kda_workspace_and_rejects(lib):
     assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 128, 64, 128, 128,
                            7, 0.1, None, None) == _hip.PF_ERR_ARG                        # no such dtype
     assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 64, 64, 128, 128,
-                           1, 0.1, None, None) == _hip.PF_ERR_ARG                        # bf16, one chunk
+                           1, 0.1, None, None) == _hip.PF_ERR_WORKSPACE                  # bf16, one chunk
+    assert lib.pf_kda_exec(None, None, None, None, None, None, None, None, 1, 1, 64, 64, 128, 64,
+                           1, 0.1, None, None) == _hip.PF_ERR_ARG                        # dv 64
 
 
 def test_exec_rejects_contract_violations_before_launch(lib):
@@ -176,5 +190,5 @@ def test_ops_validate_on_host():
         kda_chunk_forward(qb, qb, qb, torch.zeros(1, 1, 128), gk)
     with pytest.raises(ValueError, match="bfloat16 or float32"):
         kda_chunk_forward(qb.half(), qb.half(), qb.half(), torch.zeros(1, 1, 128), gk)
-    with pytest.raises(ValueError, match="two chunks"):
-        kda_chunk_forward(qb[:, :, :64], qb[:, :, :64], qb[:, :, :64], torch.zeros(1, 1, 64), gk[:, :, :64])
+    with pytest.raises(ValueError, match="multiple of the chunk size"):
+        kda_chunk_forward(qb[:, :, :96], qb[:, :, :96], qb[:, :, :96], torch.zeros(1, 1, 96), gk[:, :, :96])

@@ -117,10 +117,10 @@ def test_gdn_bf16_short_sequences(B, H, T, h0):
     _check(f"GDN bf16 B{B} H{H} T{T}{' h0' if h0 else ''}", o, h, o_ref, h_ref, bf16=True)
 
 
-def _gate_case(name, T, seed):
-    """Per-token log decay g [1, 2, T] for the score-gate cases of the scan kernel."""
+def _gate_case(name, T, seed, B=1, H=2):
+    """Per-token log decay g [B, H, T] for the score-gate cases of the scan kernel."""
     gen = torch.Generator().manual_seed(seed)
-    x = torch.randn(1, 2, T, generator=gen)
+    x = torch.randn(B, H, T, generator=gen)
     sp = torch.nn.functional.softplus
     if name == "mixed_sign":          # g > 0 in places: the clamp of e^{min(G_i - G_j, 0)} acts
         return x * 0.05 - 0.03
@@ -149,6 +149,59 @@ def test_gdn_bf16_score_gates(name):
     o_ref, h_ref = _oracle(inp)
     assert np.isfinite(o).all() and np.isfinite(h).all()
     _check(f"GDN bf16 score gates {name}", o, h, o_ref, h_ref, bf16=True)
+
+
+# The scan launcher takes 32-column state slices (four workgroups per chain) when B*H >= 64, the
+# headline's instantiation, and 16-column slices below that; the tests above at B*H <= 6 run the
+# 16-column kernel.  The cases below run the 32-column one at its edges: one, two and three
+# chunks per chain (the loaders' end-of-chain clamps), a nonzero h0, both score-gate paths, and
+# B*H not a multiple of 8 (the slice mapping without XCD grouping).
+@pytest.mark.parametrize("T", [64, 128, 192, 1024])
+def test_gdn_bf16_wide_slices_h0(T):
+    B, H = 4, 16
+    announce(f"GDN bf16 32-column slices B{B} H{H} T{T} h0")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.bfloat16, seed=40 + T, h0_std=0.02)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    _check(f"GDN bf16 B{B} H{H} T{T} h0 (32-col)", o, h, o_ref, h_ref, bf16=True)
+
+
+@pytest.mark.parametrize("name", ["mixed_sign", "steep", "near_limit", "alternating"])
+def test_gdn_bf16_wide_slices_score_gates(name):
+    """Both score-gate paths (factor tables, per element) in the 32-column kernel."""
+    B, H, T = 4, 16, 1024
+    announce(f"GDN bf16 score gates {name} B{B} H{H} T{T} (32-col)")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.bfloat16, seed=13, h0_std=0.02)
+    inp["g"] = _gate_case(name, T, 14, B, H).float()
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    assert np.isfinite(o).all() and np.isfinite(h).all()
+    _check(f"GDN bf16 score gates {name} B{B} H{H} (32-col)", o, h, o_ref, h_ref, bf16=True)
+
+
+@pytest.mark.parametrize("B,H,T", [(3, 22, 512), (5, 13, 192)])
+def test_gdn_bf16_wide_slices_unaligned_chains(B, H, T):
+    """B*H = 66 and 65: 32-column slices, chains not grouped by XCD (B*H % 8 != 0)."""
+    announce(f"GDN bf16 B{B} H{H} T{T} h0 (32-col, B*H % 8 != 0)")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.bfloat16, seed=B * 50 + H,
+                            h0_std=0.02)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    _check(f"GDN bf16 B{B} H{H} T{T} h0 (32-col)", o, h, o_ref, h_ref, bf16=True)
+
+
+@pytest.mark.parametrize("B,H,T", [(4, 16, 1024), (1, 2, 256)])
+def test_deltanet_bf16_fused(B, H, T):
+    """DeltaNet (g = None) through the fused bf16 forward, against deltanet_reference
+    (forwards/deltanet.py:114-143 of the reference): the 32- and the 16-column scan."""
+    announce(f"DeltaNet bf16 fused B{B} H{H} T{T}")
+    inp = make_delta_inputs(B, H, T, kind="deltanet", dtype=torch.bfloat16, seed=60 + H)
+    assert inp["g"] is None
+    o, h = _run(inp)
+    x = as_oracle_inputs(inp)
+    ref = deltanet_reference(x["q"], x["k"], x["v"], x["beta"], C=64, dtype=np.float64)
+    _check(f"DeltaNet bf16 fused B{B} H{H} T{T}", o, h, ref["o"].reshape(o.shape), ref["final"],
+           bf16=True)
 
 
 def test_gdn_bf16_config2():

@@ -46,8 +46,8 @@ def _oracle(inp, dtype=np.float64):
     return kda_reference(x["q"], x["k"], x["v"], x["beta"], x["g"], C=64, h0=x["h0"], dtype=dtype)
 
 
-@pytest.mark.parametrize("B,H,T,h0", [(1, 2, 128, False), (2, 3, 256, True), (1, 4, 1024, True),
-                                      (1, 1, 192, False)])
+@pytest.mark.parametrize("B,H,T,h0", [(1, 3, 64, True), (2, 2, 64, False), (1, 2, 128, False),
+                                      (2, 3, 256, True), (1, 4, 1024, True), (1, 1, 192, False)])
 def test_kda_bf16_matches_oracle(B, H, T, h0):
     announce(f"KDA bf16 B{B} H{H} T{T} h0={h0}")
     inp = make_delta_inputs(B, H, T, kind="kda", dtype=torch.bfloat16, seed=B * 31 + H * 7 + T,

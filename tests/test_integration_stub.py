@@ -104,7 +104,7 @@ def test_stub_registry_opens_the_library_and_runs_setup_teardown(stub):
     assert os.path.samefile(lib._name, _hip.lib_path())
     # an unsupported shape is refused by reserve before any allocation
     assert lib.pf_gdn_reserve(kernels["gdn_forward"]._ws, 1, 1, 100, 64, 128, 128, 1) == -1
-    assert lib.pf_kda_reserve(kernels["kda_forward"]._ws, 1, 1, 64, 64, 128, 128, 1) == -1
+    assert lib.pf_kda_reserve(kernels["kda_forward"]._ws, 1, 1, 96, 64, 128, 128, 1) == -1
     reg.close()
     assert not reg._cache
 

@@ -67,12 +67,12 @@ def test_whole_forward_matches_only_its_family_and_supported_shapes():
     # KDA at C = 128: one 128-token chunk is two kernel chunks
     assert FuseKdaForward(1, 2, 1, 128, 128).match(
         canonicalize(build_kda_program(1, 2, 1, 128, 128, SCALE))) == 1
-    # the fused KDA forward runs fp32 operands at any length, bf16 from two chunks on
+    # the fused KDA forward runs bf16 and fp32 operands at any length, one chunk included
     assert FuseKdaForward(1, 2, 2, 64, 128, work=torch.float32).match(kda) == 1
     assert FuseKdaForward(1, 2, 1, 64, 128, work=torch.float32).match(
         canonicalize(build_kda_program(1, 2, 1, 64, 128, SCALE, work=torch.float32))) == 1
     assert FuseKdaForward(1, 2, 1, 64, 128).match(
-        canonicalize(build_kda_program(1, 2, 1, 64, 128, SCALE))) == 0
+        canonicalize(build_kda_program(1, 2, 1, 64, 128, SCALE))) == 1
     # fp32 GDN runs the fp32 fused path
     assert FuseGdnForward(1, 2, 2, 64, 128, work=torch.float32).match(gdn) == 1
     # DeltaNet's program has no gate coefficients: not a whole-forward site

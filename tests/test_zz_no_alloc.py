@@ -40,7 +40,10 @@ def _with_workspace(d, o, hf, B, H, T, dtype, code):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_static_forward_matches_workspace_forward(dtype):
     code = _hip.PF_DTYPE_BF16 if dtype == torch.bfloat16 else _hip.PF_DTYPE_F32
-    for B, H, T, seed in ((2, 8, 1024, 21), (1, 4, 256, 22)):      # the second call is smaller
+    # bf16 starts at the headline shape (4096 chunks: the 32-column scan, most of the scratch);
+    # each later call is smaller
+    calls = ((4, 16, 4096, 20),) if dtype == torch.bfloat16 else ()
+    for B, H, T, seed in calls + ((2, 8, 1024, 21), (1, 4, 256, 22)):
         announce(f"pf_gdn_exec_static vs pf_gdn_exec {dtype} B{B} H{H} T{T}")
         d = make_delta_inputs(B, H, T, kind="gdn", dtype=dtype, seed=seed, h0_std=0.02, device=DEV)
         outs = {}
