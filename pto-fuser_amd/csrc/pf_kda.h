@@ -12,16 +12,13 @@
 // Stage 1 (kda_local_kernel, one workgroup per chunk) does everything that does not depend on S:
 // the cumsum, the gated operands, A, the inverse, W, U and the score P; it writes W, U,
 // QE = scale q e^G, KR = k e^{G_last - G}, P = causal_incl(QE b^T) (bf16) and the chunk decay
-// e^{G_last} (fp32).  Stage 2 (kda_scan_kernel, one workgroup per (chain, 32-column slice))
-// carries S in registers through the chain:
+// e^{G_last} (fp32).  Stage 2 (kda_scan_split_kernel, pf_kda_scan.h, one workgroup per (chain,
+// 32-column slice)) carries S in registers through the chain:
 //
 //   Y = W S,  v_new = U - Y,  o^T = v_new^T P^T + (QE S)^T,  S <- e^{G_last} (.) S + KR^T v_new
 //
 // so its chunk images hold the already-gated operands and the per-channel decay is one multiply
-// of the state rows per chunk.  Two compute waves each hold 16 state columns through the whole
-// chain; four loader waves keep three chunks in flight in registers, write each chunk into the
-// free half of a double-buffered LDS stage (swizzled rows, 16-byte stores) and store the o tiles
-// the compute waves stage in LDS.
+// of the state rows per chunk.
 #pragma once
 
 #include "pf_chunk_local.h"
@@ -302,257 +299,5 @@ struct KdaScanArgs {
   int BH;
   int NC;
 };
-
-// LDS image of one chunk (C = 64, DK = 128, 32-column tile).  W, QE, KR: the GDN k / q layout
-// (288-byte rows, Swz<2,3>); P: 144-byte rows, half swap on row bit 3; U: the tile's 32 columns,
-// 96-byte rows, read transposed.
-template <int C, int DK, int TW>
-struct KdaStage {
-  static constexpr int KP = DK + 16;
-  static constexpr int TP = C + 8;
-  static constexpr int UP = TW + 16;
-  bf16 ws[C * KP];
-  bf16 qs[C * KP];
-  bf16 ks[C * KP];
-  bf16 ps[C * TP];
-  bf16 us[C * UP];
-  float dec[DK];
-};
-
-// Loader register image of one chunk: W, QE, KR 1024 vectors each; P 512; U 256; dec 32.
-template <int NLW>
-struct KdaRegs {
-  static constexpr int NK = 1024 / (64 * NLW), NP = 512 / (64 * NLW), NU = 256 / (64 * NLW);
-  uint4 w[NK], q[NK], k[NK], p[NP], u[NU];
-  uint4 d;
-};
-
-template <int C, int DK, int DV, int NLW>
-__global__ __launch_bounds__(64 * (2 + NLW)) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void kda_scan_kernel(KdaScanArgs a) {
-  constexpr int NWC = 2, TW = 32;
-  using Stage = KdaStage<C, DK, TW>;
-  using Regs = KdaRegs<NLW>;
-  constexpr int KP = Stage::KP, TP = Stage::TP, UP = Stage::UP;
-  constexpr int NT = DV / TW;
-  static_assert(C == 64 && DK == 128 && NLW == 4, "tile shapes of the KDA scan kernel are fixed");
-
-  __shared__ __attribute__((aligned(16))) Stage st[2];
-  constexpr int OP = TW + 4;
-  __shared__ __attribute__((aligned(16))) float ost[2][C * OP];
-
-  int bh, tile;
-  const int bid = blockIdx.x;
-  if (a.BH % 8 == 0) {  // the NT tiles of one chain share an XCD (dispatch is round-robin on XCDs)
-    const int grp = bid / (8 * NT), within = bid % (8 * NT);
-    bh = grp * 8 + (within % 8);
-    tile = within / 8;
-  } else {
-    bh = bid / NT;
-    tile = bid % NT;
-  }
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
-  const int NC = a.NC;
-  const int col0 = tile * TW;
-  const uint32_t Tlen = (uint32_t)NC * C;
-
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.W + (size_t)bh * Tlen * DK, Tlen * DK * 2);
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.QE + (size_t)bh * Tlen * DK, Tlen * DK * 2);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.KR + (size_t)bh * Tlen * DK, Tlen * DK * 2);
-  const __amdgpu_buffer_rsrc_t ru = make_rsrc(a.U + (size_t)bh * Tlen * DV, Tlen * DV * 2);
-  const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.P + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
-  const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.DEC + (size_t)bh * NC * DK, (uint32_t)NC * DK * 4);
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.o + (size_t)bh * Tlen * DV, Tlen * DV * 4);
-
-  if (w >= NWC) {
-    // =========================== loader waves ===========================
-    const int lt = tid - 64 * NWC;
-    __builtin_amdgcn_s_setprio(3);
-    // W / QE / KR rows (16 vectors per row): row = a0 | a1<<1 | i0<<2 | a2<<3 | a3<<4 | i1<<5
-    const int ka = lt >> 4, kvec = lt & 15;
-    const int krow_l = (ka & 3) | (((ka >> 2) & 1) << 3) | ((ka >> 3) << 4);
-    const uint32_t k_voff = (uint32_t)(krow_l * DK + kvec * 8) * 2;
-    const int k_lds = krow_l * KP + 8 * (kvec ^ ((ka >> 2) & 1));   // Swz<2,3>: slot ^= row bit 3
-    auto krow_i = [](int i) -> int { return ((i & 1) << 2) | (((i >> 1) & 1) << 5); };
-    // P rows (8 vectors per row): row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | a4<<5
-    const int ta = lt >> 3, tvec = lt & 7;
-    const int prow_l = (ta & 7) | ((ta >> 3) << 4);
-    const uint32_t p_voff = (uint32_t)(prow_l * C + tvec * 8) * 2;
-    const int p_lds = prow_l * TP + 8 * tvec;
-    auto prow_i = [](int i) -> int { return (i & 1) << 3; };
-    // U tile (4 vectors per row): row = lt >> 2, columns col0 + 8 (lt & 3)
-    const int urow = lt >> 2, uvec = lt & 3;
-    const uint32_t u_voff = (uint32_t)(urow * DV + col0 + uvec * 8) * 2;
-    // dec: 32 vectors of 4 floats (lanes 32.. repeat lanes 0..31: no branch around a load)
-    const uint32_t d_voff = (uint32_t)(lt & 31) * 16;
-
-    auto load_chunk = [&](Regs& r, int ch) {
-      const uint32_t k_s = (uint32_t)ch * C * DK * 2;
-#pragma unroll
-      for (int i = 0; i < Regs::NK; ++i) {
-        const uint32_t rowi = krow_i(i);
-        r.w[i] = buf_load16(rw, k_voff, k_s + rowi * DK * 2);
-        r.q[i] = buf_load16(rq, k_voff, k_s + rowi * DK * 2);
-        r.k[i] = buf_load16(rk, k_voff, k_s + rowi * DK * 2);
-      }
-      const uint32_t p_s = (uint32_t)ch * C * C * 2;
-#pragma unroll
-      for (int i = 0; i < Regs::NP; ++i) r.p[i] = buf_load16(rp, p_voff, p_s + prow_i(i) * C * 2);
-      const uint32_t u_s = (uint32_t)ch * C * DV * 2;
-#pragma unroll
-      for (int i = 0; i < Regs::NU; ++i) r.u[i] = buf_load16(ru, u_voff, u_s + (uint32_t)(16 * NLW * i) * DV * 2);
-      r.d = buf_load16(rd, d_voff, (uint32_t)ch * DK * 4);
-    };
-    auto store_chunk = [&](Stage& s, const Regs& r) {
-#pragma unroll
-      for (int i = 0; i < Regs::NK; ++i) {
-        const int rowi = krow_i(i);
-        put16(s.ws + k_lds + rowi * KP, r.w[i], (i & 1) != 0);
-        put16(s.qs + k_lds + rowi * KP, r.q[i], (i & 1) != 0);
-        put16(s.ks + k_lds + rowi * KP, r.k[i], (i & 1) != 0);
-      }
-#pragma unroll
-      for (int i = 0; i < Regs::NP; ++i) put16(s.ps + p_lds + prow_i(i) * TP, r.p[i], (i & 1) != 0);
-#pragma unroll
-      for (int i = 0; i < Regs::NU; ++i) *reinterpret_cast<uint4*>(s.us + (urow + 16 * NLW * i) * UP + 8 * uvec) = r.u[i];
-      if (lt < 32) *reinterpret_cast<uint4*>(s.dec + 4 * lt) = r.d;
-    };
-    const int orow_l = lt >> 3, oseg = lt & 7;
-    const uint32_t o_voff = (uint32_t)(orow_l * DV + col0 + 4 * oseg) * 4;
-    auto store_o = [&](const float* os, int ch) {
-#pragma unroll
-      for (int i = 0; i < (C * TW / 4) / (64 * NLW); ++i) {
-        const int row = orow_l + (64 * NLW / 8) * i;
-        const floatx4 x = *reinterpret_cast<const floatx4*>(os + row * OP + 4 * oseg);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro, o_voff + (uint32_t)((64 * NLW / 8) * i * DV) * 4,
-                                               (uint32_t)ch * C * DV * 4, kCachePolicyNT);   // streamed
-      }
-    };
-    // Same schedule as the GDN scan kernel: step j (between barriers j and j+1) issues the loads
-    // of chunk j+2, writes out the o of chunk j-2, stores chunk j into buffer j & 1; three
-    // register sets rotate.  The compute waves pass NC + 1 barriers (one before the first chunk,
-    // one after each); so do the loaders: barrier 1, the steps 1 .. NC-1, barrier NC + 1.  With
-    // one chunk there is no step and no o two chunks back.
-    const int last = NC - 1;
-    Regs r0, r1, r2;
-    auto step = [&](Regs& ld, Regs& sd, int j, bool with_o) {
-      load_chunk(ld, min(j + 2, last));
-      if (with_o) store_o(ost[j & 1], j - 2);
-      store_chunk(st[j & 1], sd);
-      lds_barrier();
-    };
-    load_chunk(r0, 0);
-    load_chunk(r1, min(1, last));
-    load_chunk(r2, min(2, last));
-    store_chunk(st[0], r0);
-    lds_barrier();                                       // barrier 1
-    if (NC > 1) {
-      step(r0, r1, 1, false);
-      int j = 2;
-      for (; j + 2 < NC; j += 3) {
-        step(r1, r2, j, true);
-        step(r2, r0, j + 1, true);
-        step(r0, r1, j + 2, true);
-      }
-      if (j < NC) step(r1, r2, j, true);
-      if (j + 1 < NC) step(r2, r0, j + 1, true);
-      store_o(ost[NC & 1], NC - 2);
-    }
-    lds_barrier();                                       // barrier NC + 1
-    store_o(ost[(NC - 1) & 1], NC - 1);
-  } else {
-    // =========================== compute waves ===========================
-    const int cbase = 16 * w;
-    const int colw = col0 + cbase + c;
-    const int kq_rd = c * KP + 4 * (g ^ ((c >> 2) & 3));             // W / QE rows, permuted K
-    const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g);   // transposed A of KR^T
-    const int tp_rd = c * TP + 4 * (g ^ (c >> 3));                   // P rows, permuted K
-    const int u_rd = (4 * g + (c >> 2)) * UP + cbase + 4 * (c & 3);  // transposed U column
-    const int o_lds = c * OP + cbase + 4 * g;
-
-    floatx4 S[DK / 16];
-#pragma unroll
-    for (int r = 0; r < DK / 16; ++r)
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii)
-        S[r][ii] = a.h0 ? a.h0[((size_t)bh * DK + 16 * r + 4 * g + ii) * DV + colw] : 0.f;
-
-    auto compute_chunk = [&](const Stage& s, int ch) {
-      bf16x8 SB[DK / 32];
-#pragma unroll
-      for (int kb = 0; kb < DK / 32; ++kb) SB[kb] = pack8(S[2 * kb], S[2 * kb + 1]);
-      floatx4 Y[4], QT[4], VN[4];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        Y[mb] = zero4();
-        QT[mb] = zero4();
-      }
-#pragma unroll
-      for (int kb = 0; kb < DK / 32; ++kb) {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const bf16* wp = s.ws + kq_rd + 16 * mb * KP + 32 * kb;
-          const bf16* qp = s.qs + kq_rd + 16 * mb * KP + 32 * kb;
-          const bf16x8 wa = cat8(*reinterpret_cast<const bf16x4*>(wp), *reinterpret_cast<const bf16x4*>(wp + 16));
-          const bf16x8 qa = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
-          Y[mb] = mfma_bf16(wa, SB[kb], Y[mb]);        // (W S)[t][n]
-          QT[mb] = mfma_bf16(SB[kb], qa, QT[mb]);      // (QE S)^T[n][t]
-        }
-      }
-      // v_new = U - W S
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const bf16x4 uu = lds_read_tr(s.us + u_rd + 16 * mb * UP);
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) VN[mb][ii] = (float)uu[ii] - Y[mb][ii];
-      }
-      const bf16x8 VB0 = pack8(VN[0], VN[1]), VB1 = pack8(VN[2], VN[3]);
-      // o^T = v_new^T P^T + (QE S)^T
-      float* os = ost[ch & 1];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const bf16* pp = s.ps + tp_rd + 16 * mb * TP;
-        const bf16x8 p0 = cat8(*reinterpret_cast<const bf16x4*>(pp), *reinterpret_cast<const bf16x4*>(pp + 16));
-        floatx4 OT = mfma_bf16(VB0, p0, QT[mb]);
-        if (mb >= 2) {
-          const bf16x8 p1 = cat8(*reinterpret_cast<const bf16x4*>(pp + 32), *reinterpret_cast<const bf16x4*>(pp + 48));
-          OT = mfma_bf16(VB1, p1, OT);
-        }
-        *reinterpret_cast<floatx4*>(os + o_lds + 16 * mb * OP) = OT;
-      }
-      // S <- e^{G_last} (.) S + KR^T v_new  (the decay scales the state rows = key channels)
-#pragma unroll
-      for (int r = 0; r < DK / 16; ++r) {
-        const floatx4 d4 = *reinterpret_cast<const floatx4*>(s.dec + 16 * r + 4 * g);
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) S[r][ii] *= d4[ii];
-      }
-#pragma unroll
-      for (int r = 0; r < DK / 16; ++r) {
-        const bf16* k0 = s.ks + kt_rd + 16 * r;
-        const bf16x8 a0 = cat8(lds_read_tr(k0), lds_read_tr(k0 + 16 * KP));
-        const bf16x8 a1 = cat8(lds_read_tr(k0 + 32 * KP), lds_read_tr(k0 + 48 * KP));
-        const floatx4 acc = mfma_bf16(a0, VB0, S[r]);
-        S[r] = mfma_bf16(a1, VB1, acc);
-      }
-    };
-
-    lds_barrier();
-    for (int ch = 0; ch < NC; ch += 2) {
-      compute_chunk(st[0], ch);
-      lds_barrier();
-      if (ch + 1 >= NC) break;
-      compute_chunk(st[1], ch + 1);
-      lds_barrier();
-    }
-    if (a.h_final) {
-#pragma unroll
-      for (int r = 0; r < DK / 16; ++r)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-          a.h_final[((size_t)bh * DK + 16 * r + 4 * g + ii) * DV + colw] = S[r][ii];
-    }
-  }
-}
 
 }  // namespace pf

@@ -5,6 +5,7 @@
 
 #include "../../include/pto_fuser_hip.h"
 #include "pf_kda.h"
+#include "pf_kda_scan.h"
 #include "pf_kda_f32.h"
 #include "pf_status.h"
 #include "pf_workspace.h"
@@ -150,7 +151,7 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   sa.NC = T / kChunk;
   constexpr int NLW = 4;
   const unsigned grid = (unsigned)(B * H * (KD / 32));
-  pf::kda_scan_kernel<KC, KD, KD, NLW><<<dim3(grid), dim3(64 * (2 + NLW)), 0, s>>>(sa);
+  pf::kda_scan_split_kernel<KC, KD, KD, NLW><<<dim3(grid), dim3(64 * (4 + NLW)), 0, s>>>(sa);
   return scope.status();
 }
 
