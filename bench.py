@@ -28,7 +28,9 @@ Besides the required fields the line carries:
     workspace: 90 624 B per chunk + the final state).  ``traffic`` is the counter-measured HBM
     bytes per launch recorded in profiles/hbm_traffic_gdn_forward.json, reported only when that
     record was taken from the library built from the current sources (its source hash), else
-    null;
+    null; ``kernel_avg_ms_rocprof`` / ``frac_rocprof`` are the kernel's rocprofv3 kernel-trace
+    average (profiles/kernel_trace_gdn_forward.json, same source-hash rule) and the fraction
+    recomputed from it;
   * ``stages`` — both kernels' average durations, bytes and flops, and their HBM / MFMA fractions;
   * ``forward`` — the whole forward's compulsory-byte and flop fractions at ``ms_per_step``,
     and the timed loop run REPEATS more times (``repeats_ms_per_step``, their median);
@@ -62,6 +64,7 @@ PEAK_BF16 = 2.5e15         # dense bf16 MFMA, flop/s
 PEAK_FP32 = 157.3e12       # dense fp32 MFMA, flop/s
 METRIC = "GDN chunked-forward tokens/sec at B=4,H=16,T=4096 bf16; % MFMA/HBM roofline"
 COUNTERS = os.path.join(ROOT, "profiles", "hbm_traffic_gdn_forward.json")
+TRACE = os.path.join(ROOT, "profiles", "kernel_trace_gdn_forward.json")
 
 
 def measured_traffic(kernel, lib_hash):
@@ -81,6 +84,55 @@ def measured_traffic(kernel, lib_hash):
     return int(sum(kib[c] * rec["scale"][c] * 1024 for c in ("FETCH_SIZE", "WRITE_SIZE")))
 
 
+def traced_kernel_ms(kernel, lib_hash):
+    """Average duration (ms) of ``kernel`` in the recorded rocprofv3 kernel trace, or None when
+    no record exists for the library built from the current sources."""
+    try:
+        with open(TRACE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("source_hash") != lib_hash:
+        return None
+    k = rec.get("kernels", {}).get(kernel)
+    return None if k is None else k["avg_us"] / 1e3
+
+
+def summarize_trace(trace_csv, lib_hash, out=None):
+    """Write the kernel-trace record bench.py reads (``TRACE``) from the kernel_trace.csv of a
+    ``rocprofv3 --kernel-trace --stats --output-format csv`` run of bench.py: per kernel (the keys
+    of the counter record) the dispatch count and the average, median, min and max duration,
+    tagged with the library's source hash."""
+    import csv
+    durs = {}
+    with open(trace_csv) as f:
+        for row in csv.DictReader(f):
+            name = row["Kernel_Name"]
+            if "Grid_Size" in row:
+                grid = int(row["Grid_Size"])
+            else:
+                grid = int(row["Grid_Size_X"]) * int(row.get("Grid_Size_Y", 1)) * int(row.get("Grid_Size_Z", 1))
+            key = _counter_key(name, grid)
+            if key is not None:
+                durs.setdefault(key, []).append(
+                    (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    kernels = {}
+    for key, v in durs.items():
+        v.sort()
+        kernels[key] = {"dispatches": len(v), "avg_us": round(statistics.mean(v), 3),
+                        "median_us": round(v[len(v) // 2], 3), "min_us": round(v[0], 3),
+                        "max_us": round(v[-1], 3)}
+    rec = {"workload": "GDN forward B4 H16 T4096 C64 dk=dv=128, bf16 in (bench.py headline); "
+                       "long_*: bench.py gdn_config4_long_context; kda_*: bench.py kda_config5",
+           "source_hash": lib_hash,
+           "command": "rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o kt -- "
+                      "python3 bench.py --steps 50 --warmup 10 --no-cpu-baseline",
+           "kernels": kernels}
+    with open(out or TRACE, "w") as f:
+        json.dump(rec, f, indent=1)
+    return rec
+
+
 def _counter_key(name, grid):
     """Record key of a dispatch in the counter passes: the headline's two kernels (the 32-column
     scan and the 4096-chunk stage 1), the long-context secondary's two (the 16-column scan and
@@ -93,9 +145,10 @@ def _counter_key(name, grid):
         return "scan_output"
     if "scan_split_kernel<64, 128, 128, 1," in name:
         return "long_scan_output"
-    if "chunk_local_kernel" in name and "DF16b" in name and grid == M * 256:
+    bf16 = "DF16b" in name or "bf16" in name          # __bf16 as the demangler spells it
+    if "chunk_local_kernel" in name and bf16 and grid == M * 256:
         return "chunk_local"
-    if "chunk_local_kernel" in name and "DF16b" in name and grid == ML * 256:
+    if "chunk_local_kernel" in name and bf16 and grid == ML * 256:
         return "long_chunk_local"
     for k in ("kda_scan", "kda_local"):
         if k in name:
@@ -359,6 +412,8 @@ def main(argv=None) -> int:
     ap.add_argument("--summarize-counters", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="write the counter record from two rocprofv3 --pmc result databases "
                          "(FETCH_SIZE, WRITE_SIZE) of a --calibrate-copy run, then exit")
+    ap.add_argument("--summarize-trace", metavar="TRACE_CSV",
+                    help="write the kernel-trace record from a rocprofv3 kernel_trace.csv, then exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run three plain device copies of MIB MiB: the "
                          "known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -371,6 +426,11 @@ def main(argv=None) -> int:
               f"communication, so per-GPU throughput at N GPUs is the N=1 figure.",
               file=sys.stderr)
         return 2
+    if args.summarize_trace:
+        from pto_fuser_amd import _build
+        rec = summarize_trace(args.summarize_trace, _build.source_hash())
+        print(json.dumps(rec["kernels"]))
+        return 0
     if args.summarize_counters:
         from pto_fuser_amd import _build
         rec = summarize_counters(*args.summarize_counters, _build.source_hash(),
@@ -472,6 +532,7 @@ def main(argv=None) -> int:
         }
     ds = stages["scan_output"]
     k2 = k2_ms * 1e-3
+    k2_trace_ms = traced_kernel_ms("scan_output", lib_hash)
     roofline = {"kernel": "scan_output", "bound": "hbm",
                 "achieved": round(comp / k2 / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                 "frac": round(comp / k2 / PEAK_HBM, 4), "traffic": ds["traffic"],
@@ -481,6 +542,12 @@ def main(argv=None) -> int:
                 "own_frac": ds["hbm_frac"],
                 "device_copy_GBps": round(copy_GBps, 1),
                 "frac_of_device_copy": round(comp / k2 / 1e9 / copy_GBps, 4),
+                # the same kernel's average in the recorded rocprofv3 kernel trace
+                # (profiles/kernel_trace_gdn_forward.json, same source hash), and the fraction
+                # recomputed from it
+                "kernel_avg_ms_rocprof": None if k2_trace_ms is None else round(k2_trace_ms, 5),
+                "frac_rocprof": None if k2_trace_ms is None else
+                round(comp / (k2_trace_ms * 1e-3) / PEAK_HBM, 4),
                 "source_hash": lib_hash}
     total_bytes = sum(model[n]["bytes"] for n in model)
     total_flops = sum(model[n]["flops"] for n in model)

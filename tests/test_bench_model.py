@@ -113,3 +113,29 @@ def test_multi_gpu_request_exits_with_message():
                        cwd=bench.ROOT, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_trace_record_roundtrip(tmp_path, monkeypatch):
+    """--summarize-trace groups a kernel_trace.csv by the counter keys (kernel name and grid) and
+    tags the record with the source hash; bench reads the stage-2 average back only for that
+    hash."""
+    M = 4 * 16 * 64
+    rows = [("void pf::scan_split_kernel<64, 128, 128, 2, 4>(pf::ScanOutArgs)", 256 * 512, 1000, 91000),
+            ("void pf::scan_split_kernel<64, 128, 128, 2, 4>(pf::ScanOutArgs)", 256 * 512, 2000, 91000),
+            ("void pf::chunk_local_kernel<__bf16, __bf16, 64, 128, false, true>(pf::ChunkLocalArgs)",
+             M * 256, 0, 21000),
+            ("void at::native::copy_kernel(...)", 1 << 20, 0, 5000)]
+    csv_path = tmp_path / "kt_kernel_trace.csv"
+    with open(csv_path, "w") as f:
+        f.write('"Kernel_Name","Grid_Size","Start_Timestamp","End_Timestamp"\n')
+        for name, grid, t0, t1 in rows:
+            f.write(f'"{name}",{grid},{t0},{t1}\n')
+    out = tmp_path / "trace.json"
+    monkeypatch.setattr(bench, "TRACE", str(out))
+    rec = bench.summarize_trace(str(csv_path), "abc123")
+    assert rec["kernels"]["scan_output"]["dispatches"] == 2
+    assert rec["kernels"]["scan_output"]["avg_us"] == pytest.approx(89.5)
+    assert rec["kernels"]["chunk_local"]["avg_us"] == pytest.approx(21.0)
+    assert set(rec["kernels"]) == {"scan_output", "chunk_local"}
+    assert bench.traced_kernel_ms("scan_output", "abc123") == pytest.approx(0.0895)
+    assert bench.traced_kernel_ms("scan_output", "other") is None
