@@ -1,0 +1,193 @@
+// Memory floor of the scan kernels' access patterns on gfx950: a measurement probe, not part of
+// libptofuser_hip (built as its own executable next to the library).
+//
+// Each stage-2 scan workgroup (one chain x one column slice, one workgroup per CU) streams a
+// chunk image per step from HBM through registers into a double-buffered LDS stage (its loader
+// waves: three rotating register sets, a chunk's loads issued three steps ahead, one LDS store
+// per 16-byte vector) and writes its o rows.  The column slices of one chain sit on one XCD and
+// read the same image.  This probe runs exactly that traffic with no compute: 256 workgroups of
+// four loader waves, SH workgroups on an XCD (blockIdx % 8) sharing each image, OB bytes of o rows
+// per workgroup and step (each slice OB / 64 bytes of every token's row, non-temporal or
+// through the cache as the kernel stores them).  The time per step is the shortest chunk period
+// those loads and stores allow; it is printed for each kernel's pattern with the loads alone and
+// the stores alone beside it, together with the shader clock the probe ran at (s_memtime against
+// s_memrealtime's 100 MHz).
+//
+// Every offset stays inside its buffer (descriptors carry each region's size; steps clamp).
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstdio>
+
+namespace {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSteps = 96;        // chunks streamed per launch
+constexpr int kGroups = 256;      // one workgroup per CU
+constexpr int kMaxKiB = 64;       // largest chunk image (LDS: two stages)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// KIB: 16-byte loads per workgroup and chunk (KiB, a multiple of 4: wave w loads the 1 KiB
+// vectors w, w + 4, ..., every wave the same number, with no branch around a load, as the
+// kernels' loaders do; where a kernel's lanes repeat a vector, the repeat is counted);
+// SH: workgroups sharing one image; OB: o bytes per workgroup and step (0: none); NTST: o stores
+// non-temporal; LD: issue the loads.
+template <int KIB, int SH, int OB, bool NTST, bool LD>
+__global__ __launch_bounds__(256) void floor_kernel(const unsigned char* src, unsigned char* dst,
+                                                    uint32_t* sink, unsigned long long* clocks) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2][kMaxKiB * 1024];
+  static_assert(KIB % 4 == 0 && KIB <= kMaxKiB, "chunk image: whole 4 KiB rounds");
+  constexpr int N = KIB / 4;                          // 1 KiB loads per wave and step
+  constexpr uint32_t kStep = KIB * 1024;
+  constexpr uint32_t kRegion = kStep * kSteps;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int x = blockIdx.x % 8, i = blockIdx.x / 8;
+  const int region = x * (32 / SH) + i / SH;          // the chain this workgroup's slice reads
+  const int slice = i % SH;
+  const __amdgpu_buffer_rsrc_t r = rsrc(src + (size_t)region * kRegion, kRegion);
+  constexpr uint32_t kOBytes = (OB > 0 ? OB : 64) * SH * kSteps;   // o rows of one chain
+  const __amdgpu_buffer_rsrc_t ro = rsrc(dst + (size_t)region * kOBytes, kOBytes);
+
+  struct Set { u32x4 v[N]; };
+  auto load = [&](Set& s, int step) {
+    if constexpr (LD) {
+#pragma unroll
+      for (int k = 0; k < N; ++k)
+        s.v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, 16 * lane, (uint32_t)step * kStep + (4 * k + w) * 1024, 0);
+    }
+  };
+  auto stage = [&](int buf, const Set& s) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) *reinterpret_cast<u32x4*>(lds[buf] + (4 * k + w) * 1024 + 16 * lane) = s.v[k];
+  };
+  auto ostore = [&](int step) {
+    if constexpr (OB > 0) {
+      // 64 tokens per step; this slice's BPT bytes of each token's (BPT * SH)-byte row; a store
+      // instruction covers 1 KiB (TPI tokens), wave w tokens 16 w .. 16 w + 15
+      constexpr int BPT = OB / 64, LPT = BPT / 16, TPI = 64 / LPT;
+      const u32x4 val = {(uint32_t)step, 1u, 2u, 3u};
+#pragma unroll
+      for (int k = 0; k < 16 / TPI; ++k) {
+        const uint32_t tok = (uint32_t)step * 64 + 16 * w + TPI * k + lane / LPT;
+        __builtin_amdgcn_raw_buffer_store_b128(val, ro, tok * BPT * SH + BPT * slice + 16 * (lane % LPT), 0,
+                                               NTST ? 2 : 0);
+      }
+    }
+  };
+  uint32_t acc = 0;
+  auto interval = [&](Set& ld, const Set& nx, int j) {
+    load(ld, min(j + 3, kSteps - 1));
+    stage((j + 1) & 1, nx);
+    ostore(j);
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);               // LDS stores landed; loads stay in flight
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+    acc += lds[j & 1][(threadIdx.x * 16) % kStep];
+  };
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  Set s0, s1, s2;
+  load(s0, 0);
+  load(s1, 1);
+  load(s2, 2);
+  stage(0, s0);
+  __syncthreads();
+  interval(s0, s1, 0);
+  for (int j = 1; j + 3 < kSteps; j += 3) {
+    interval(s1, s2, j);
+    interval(s2, s0, j + 1);
+    interval(s0, s1, j + 2);
+  }
+  sink[blockIdx.x * 256 + threadIdx.x] = acc;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    clocks[0] = __builtin_amdgcn_s_memtime() - t0;
+    clocks[1] = __builtin_amdgcn_s_memrealtime() - r0;
+  }
+}
+
+constexpr int executed_steps() {
+  int n = 1;
+  for (int j = 1; j + 3 < kSteps; j += 3) n += 3;
+  return n;
+}
+
+struct Buffers {
+  unsigned char* src;
+  unsigned char* dst;
+  uint32_t* sink;
+  unsigned long long* clocks;
+  hipEvent_t e0, e1;
+};
+
+bool ok(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    std::printf("%s failed: %s\n", what, hipGetErrorString(e));
+    return false;
+  }
+  return true;
+}
+
+// Best of four timed launches (after one warm-up) of one pattern; prints one line.
+template <int KIB, int SH, int OB, bool NTST, bool LD>
+bool run(const Buffers& b, const char* pattern, const char* what, int chain_chunks) {
+  float best = 1e30f;
+  for (int rep = 0; rep < 5; ++rep) {
+    if (!ok(hipEventRecord(b.e0), "hipEventRecord")) return false;
+    floor_kernel<KIB, SH, OB, NTST, LD><<<kGroups, 256>>>(b.src, b.dst, b.sink, b.clocks);
+    if (!ok(hipGetLastError(), "launch") || !ok(hipEventRecord(b.e1), "hipEventRecord") ||
+        !ok(hipEventSynchronize(b.e1), "hipEventSynchronize"))
+      return false;
+    float ms = 0.f;
+    if (!ok(hipEventElapsedTime(&ms, b.e0, b.e1), "hipEventElapsedTime")) return false;
+    if (rep > 0 && ms < best) best = ms;
+  }
+  unsigned long long clk[2] = {0, 0};
+  if (!ok(hipMemcpy(clk, b.clocks, sizeof(clk), hipMemcpyDeviceToHost), "hipMemcpy")) return false;
+  const double ns = best * 1e6 / executed_steps();
+  const double mhz = clk[1] ? 100.0 * (double)clk[0] / (double)clk[1] : 0.0;
+  std::printf("%-12s %-14s  %2d KiB/chunk  shared by %d  o %5d B/chunk %-3s  %7.1f ns per chunk  "
+              "%7.1f us per %d chunks  clock %4.0f MHz\n",
+              pattern, what, KIB, SH, OB, OB ? (NTST ? "nt" : "l2") : "", ns, ns * chain_chunks / 1000.0,
+              chain_chunks, mhz);
+  std::fflush(stdout);
+  return true;
+}
+
+// The three stage-2 patterns: loads and o stores, the loads alone, the stores alone.
+template <int KIB, int SH, int OB, bool NTST>
+bool pattern(const Buffers& b, const char* name, int chain_chunks) {
+  return run<KIB, SH, OB, NTST, true>(b, name, "loads+stores", chain_chunks) &&
+         run<KIB, SH, 0, NTST, true>(b, name, "loads", chain_chunks) &&
+         run<KIB, SH, OB, NTST, false>(b, name, "stores", chain_chunks);
+}
+
+}  // namespace
+
+int main() {
+  Buffers b{};
+  const size_t src_bytes = (size_t)kMaxKiB * 1024 * kSteps * (kGroups / 4);   // SH >= 4
+  const size_t dst_bytes = (size_t)8192 * kSteps * kGroups;
+  if (!ok(hipMalloc(&b.src, src_bytes), "hipMalloc") || !ok(hipMalloc(&b.dst, dst_bytes), "hipMalloc") ||
+      !ok(hipMalloc(&b.sink, kGroups * 256 * sizeof(uint32_t)), "hipMalloc") ||
+      !ok(hipMalloc(&b.clocks, 2 * sizeof(unsigned long long)), "hipMalloc") ||
+      !ok(hipMemset(b.src, 1, src_bytes), "hipMemset") || !ok(hipEventCreate(&b.e0), "hipEventCreate") ||
+      !ok(hipEventCreate(&b.e1), "hipEventCreate"))
+    return 1;
+  // GDN headline (B4 H16 T4096): 32-column slices, k 16 + q 16 + T 8 + v 4 KiB, o 32 x 4 B per
+  // token streamed past the cache.
+  if (!pattern<44, 4, 8192, true>(b, "gdn_headline", 64)) return 1;
+  // GDN config 4 (B1 H32 T32768): 16-column slices, k 16 + q 16 + T 8 KiB + the v tile (2 KiB,
+  // loaded as 4 KiB: one 16-byte load per loader lane), o 16 x 4 B per token through the cache.
+  if (!pattern<44, 8, 4096, false>(b, "gdn_config4", 512)) return 1;
+  // KDA config 5 (B2 H32 T8192): 32-column slices, W, QE, KR 16 KiB each + P 8 + U 4 KiB + the
+  // decay (one 16-byte load per loader lane: 4 KiB), o streamed past the cache.
+  if (!pattern<64, 4, 8192, true>(b, "kda_config5", 128)) return 1;
+  (void)hipFree(b.src);
+  (void)hipFree(b.dst);
+  (void)hipFree(b.sink);
+  (void)hipFree(b.clocks);
+  return 0;
+}

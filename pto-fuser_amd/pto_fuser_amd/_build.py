@@ -99,6 +99,21 @@ def build(verbose: bool = False, out: Optional[str] = None) -> str:
     return out
 
 
+PROBE_SRC = os.path.join(CSRC, "probe", "pf_memfloor.hip")
+PROBE_PATH = os.path.join(LIB_DIR, "pf_memfloor")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """Compile the memory-floor probe (``csrc/probe/pf_memfloor.hip``: the scan kernels' load and
+    store traffic with no compute, a measurement tool outside the library) into
+    ``lib/pf_memfloor``; returns its path."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = PROBE_PATH + f".tmp{os.getpid()}"
+    _run([_hipcc(), *[f for f in HIPCC_FLAGS if f != "-fPIC"], PROBE_SRC, "-o", tmp], verbose)
+    os.replace(tmp, PROBE_PATH)
+    return PROBE_PATH
+
+
 def ensure_built(verbose: bool = False) -> str:
     """Return the library path, compiling only when no library has been built yet (the GPU box
     runs the library built in this tree; it never rebuilds a present one)."""
