@@ -13,6 +13,13 @@
 // the stores alone beside it, together with the shader clock the probe ran at (s_memtime against
 // s_memrealtime's 100 MHz).
 //
+// A second form replays the kernels' own address pattern: the chunk images read from tensors laid
+// out as the kernels read them (k, q, v and o as [B*H, T, 128], T as [B*H, NC, 64, 64]; KDA's
+// W, QE, KR as [B*H, NC, 64, 128], P as [B*H, NC, 64, 64], U as [B*H, T, 128], the decay as
+// [B*H, NC, 128] fp32), with the kernels' chain-to-workgroup mapping (the slices of a chain on one
+// XCD) and each loader lane's 16-byte vectors, so the floor includes what the tensors' strides
+// (powers of two at these shapes) cost the memory system.
+//
 // Every offset stays inside its buffer (descriptors carry each region's size; steps clamp).
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -108,10 +115,121 @@ __global__ __launch_bounds__(256) void floor_kernel(const unsigned char* src, un
   }
 }
 
-constexpr int executed_steps() {
+constexpr int executed_steps(int steps = kSteps) {
   int n = 1;
-  for (int j = 1; j + 3 < kSteps; j += 3) n += 3;
+  for (int j = 1; j + 3 < steps; j += 3) n += 3;
   return n;
+}
+
+// Tensors of one workload in the kernels' layout.
+struct Tensors {
+  const unsigned char* a[6];   // GDN: k, q, T, v; KDA: W, QE, KR, P, U, decay
+  unsigned char* o;            // [chains, T, 128] fp32
+};
+
+// The kernels' traffic at their own addresses.  KDA false: GDN stage 2 (per loader wave and
+// chunk 4 k, 4 q, 2 T vectors of 1 KiB and one v load per lane); KDA true: 4 W, 4 QE, 4 KR, 2 P,
+// one U and one decay load per lane.  NCOL: columns per slice (32 or 16), NC: chunks per chain,
+// STEPS: chunks streamed, NTST: o stores non-temporal, LD / ST: issue the loads / the stores.
+template <bool KDA, int NCOL, int NC, int STEPS, bool NTST, bool LD, bool ST>
+__global__ __launch_bounds__(256) void layout_kernel(Tensors t, uint32_t* sink, int chains) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2][kMaxKiB * 1024];
+  constexpr int NS = 128 / NCOL;                    // slices per chain
+  constexpr int NV = KDA ? 16 : 11;                 // 16-byte loads per lane and chunk
+  constexpr uint32_t Tlen = NC * 64;
+  const int lane = threadIdx.x & 63, lt = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int bh, slice;
+  const int bid = blockIdx.x;
+  if (chains % 8 == 0) {                            // the kernels' XCD-aware mapping
+    const int grp = bid / (8 * NS), within = bid % (8 * NS);
+    bh = grp * 8 + within % 8;
+    slice = within / 8;
+  } else {
+    bh = bid / NS;
+    slice = bid % NS;
+  }
+  const int col0 = slice * NCOL;
+  // per-chain descriptors: rows of 128 bf16 (256 B) per token, chunk images of 16 / 8 KiB
+  const uint32_t row_bytes = Tlen * 256u;
+  const __amdgpu_buffer_rsrc_t r0 = rsrc(t.a[0] + (size_t)bh * row_bytes, row_bytes);
+  const __amdgpu_buffer_rsrc_t r1 = rsrc(t.a[1] + (size_t)bh * row_bytes, row_bytes);
+  const __amdgpu_buffer_rsrc_t r2 = rsrc(t.a[2] + (size_t)bh * (KDA ? row_bytes : NC * 8192u), KDA ? row_bytes : NC * 8192u);
+  const __amdgpu_buffer_rsrc_t r3 = rsrc(t.a[3] + (size_t)bh * (KDA ? NC * 8192u : row_bytes), KDA ? NC * 8192u : row_bytes);
+  const __amdgpu_buffer_rsrc_t r4 = rsrc(t.a[KDA ? 4 : 3] + (size_t)bh * row_bytes, row_bytes);
+  const __amdgpu_buffer_rsrc_t r5 = rsrc(t.a[KDA ? 5 : 3] + (size_t)bh * (KDA ? NC * 512u : row_bytes), KDA ? NC * 512u : row_bytes);
+  const __amdgpu_buffer_rsrc_t ro = rsrc(t.o + (size_t)bh * Tlen * 512u, Tlen * 512u);
+  // a slice's rows of a [T, 128] bf16 tile (v or U): NCOL * 2 bytes per row, 64 rows; lanes past
+  // the tile's vectors repeat (as the kernels' loaders do)
+  constexpr int VPR = NCOL / 8, VV = 64 * VPR;
+  const int vu = lt % VV;
+  const uint32_t tile_off = (uint32_t)(vu / VPR) * 256u + (uint32_t)col0 * 2u + (uint32_t)(vu % VPR) * 16u;
+
+  struct Set { u32x4 v[NV]; };
+  auto load = [&](Set& s, int ch) {
+    if constexpr (LD) {
+      const uint32_t c16 = (uint32_t)ch * 16384u, c8 = (uint32_t)ch * 8192u;
+      const uint32_t lo = 16u * lane + 1024u * w;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        s.v[k] = __builtin_amdgcn_raw_buffer_load_b128(r0, lo, c16 + 4096u * k, 0);
+        s.v[4 + k] = __builtin_amdgcn_raw_buffer_load_b128(r1, lo, c16 + 4096u * k, 0);
+      }
+      if constexpr (!KDA) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) s.v[8 + k] = __builtin_amdgcn_raw_buffer_load_b128(r2, lo, c8 + 4096u * k, 0);
+        s.v[10] = __builtin_amdgcn_raw_buffer_load_b128(r4, tile_off, (uint32_t)ch * 64u * 256u, 0);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s.v[8 + k] = __builtin_amdgcn_raw_buffer_load_b128(r2, lo, c16 + 4096u * k, 0);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) s.v[12 + k] = __builtin_amdgcn_raw_buffer_load_b128(r3, lo, c8 + 4096u * k, 0);
+        s.v[14] = __builtin_amdgcn_raw_buffer_load_b128(r4, tile_off, (uint32_t)ch * 64u * 256u, 0);
+        s.v[15] = __builtin_amdgcn_raw_buffer_load_b128(r5, 16u * (lt & 31), (uint32_t)ch * 512u, 0);
+      }
+    }
+  };
+  auto stage = [&](int buf, const Set& s) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) *reinterpret_cast<u32x4*>(lds[buf] + (4 * k + w) * 1024 + 16 * lane) = s.v[k];
+  };
+  auto ostore = [&](int ch) {
+    if constexpr (ST) {
+      // o[token][col0 .. col0 + NCOL) fp32: BPT bytes per token, wave w tokens 16 w ..
+      constexpr int BPT = NCOL * 4, LPT = BPT / 16, TPI = 64 / LPT;
+      const u32x4 val = {(uint32_t)ch, 1u, 2u, 3u};
+#pragma unroll
+      for (int k = 0; k < 16 / TPI; ++k) {
+        const uint32_t tok = (uint32_t)ch * 64u + 16u * w + TPI * k + lane / LPT;
+        __builtin_amdgcn_raw_buffer_store_b128(val, ro, tok * 512u + (uint32_t)col0 * 4u + 16u * (lane % LPT), 0,
+                                               NTST ? 2 : 0);
+      }
+    }
+  };
+  uint32_t acc = 0;
+  auto interval = [&](Set& ld, const Set& nx, int j) {
+    load(ld, min(j + 3, STEPS - 1));
+    stage((j + 1) & 1, nx);
+    ostore(j);
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+    acc += lds[j & 1][(threadIdx.x * 16) % (NV * 4096)];
+  };
+  Set s0, s1, s2;
+  load(s0, 0);
+  load(s1, 1);
+  load(s2, 2);
+  stage(0, s0);
+  __syncthreads();
+  interval(s0, s1, 0);
+  for (int j = 1; j + 3 < STEPS; j += 3) {
+    interval(s1, s2, j);
+    interval(s2, s0, j + 1);
+    interval(s0, s1, j + 2);
+  }
+  sink[blockIdx.x * 256 + threadIdx.x] = acc;
 }
 
 struct Buffers {
@@ -156,6 +274,36 @@ bool run(const Buffers& b, const char* pattern, const char* what, int chain_chun
   return true;
 }
 
+// Best of four timed launches of one kernel-layout pattern; prints one line.
+template <bool KDA, int NCOL, int NC, int STEPS, bool NTST, bool LD, bool ST>
+bool run_layout(const Buffers& b, const Tensors& t, int chains, const char* pattern, const char* what) {
+  float best = 1e30f;
+  const int groups = chains * (128 / NCOL);
+  for (int rep = 0; rep < 5; ++rep) {
+    if (!ok(hipEventRecord(b.e0), "hipEventRecord")) return false;
+    layout_kernel<KDA, NCOL, NC, STEPS, NTST, LD, ST><<<groups, 256>>>(t, b.sink, chains);
+    if (!ok(hipGetLastError(), "launch") || !ok(hipEventRecord(b.e1), "hipEventRecord") ||
+        !ok(hipEventSynchronize(b.e1), "hipEventSynchronize"))
+      return false;
+    float ms = 0.f;
+    if (!ok(hipEventElapsedTime(&ms, b.e0, b.e1), "hipEventElapsedTime")) return false;
+    if (rep > 0 && ms < best) best = ms;
+  }
+  const double ns = best * 1e6 / executed_steps(STEPS);
+  std::printf("%-12s %-14s  tensor layout, %2d chains x %d slices, %3d of %3d chunks  %7.1f ns per chunk  "
+              "%7.1f us per %d chunks\n",
+              pattern, what, chains, 128 / NCOL, STEPS, NC, ns, ns * NC / 1000.0, NC);
+  std::fflush(stdout);
+  return true;
+}
+
+template <bool KDA, int NCOL, int NC, int STEPS, bool NTST>
+bool layout_pattern(const Buffers& b, const Tensors& t, int chains, const char* name) {
+  return run_layout<KDA, NCOL, NC, STEPS, NTST, true, true>(b, t, chains, name, "loads+stores") &&
+         run_layout<KDA, NCOL, NC, STEPS, NTST, true, false>(b, t, chains, name, "loads") &&
+         run_layout<KDA, NCOL, NC, STEPS, NTST, false, true>(b, t, chains, name, "stores");
+}
+
 // The three stage-2 patterns: loads and o stores, the loads alone, the stores alone.
 template <int KIB, int SH, int OB, bool NTST>
 bool pattern(const Buffers& b, const char* name, int chain_chunks) {
@@ -185,6 +333,19 @@ int main() {
   // KDA config 5 (B2 H32 T8192): 32-column slices, W, QE, KR 16 KiB each + P 8 + U 4 KiB + the
   // decay (one 16-byte load per loader lane: 4 KiB), o streamed past the cache.
   if (!pattern<64, 4, 8192, true>(b, "kda_config5", 128)) return 1;
+
+  // The same three in the kernels' tensor layout (one allocation per tensor, sized for the
+  // largest workload: 32 chains x 32768 tokens).
+  const size_t rows = (size_t)32 * 32768 * 256;           // [B*H, T, 128] bf16, 256 MiB
+  unsigned char* ten[7] = {};
+  const size_t sizes[7] = {rows, rows, rows, rows, rows, (size_t)64 * 128 * 512, rows * 2};
+  for (int i = 0; i < 7; ++i)
+    if (!ok(hipMalloc(&ten[i], sizes[i]), "hipMalloc") || !ok(hipMemset(ten[i], 1, sizes[i]), "hipMemset")) return 1;
+  const Tensors t{{ten[0], ten[1], ten[2], ten[3], ten[4], ten[5]}, ten[6]};
+  if (!layout_pattern<false, 32, 64, 64, true>(b, t, 64, "gdn_headline")) return 1;
+  if (!layout_pattern<false, 16, 512, 96, false>(b, t, 32, "gdn_config4")) return 1;
+  if (!layout_pattern<true, 32, 128, 96, true>(b, t, 64, "kda_config5")) return 1;
+  for (int i = 0; i < 7; ++i) (void)hipFree(ten[i]);
   (void)hipFree(b.src);
   (void)hipFree(b.dst);
   (void)hipFree(b.sink);
