@@ -344,6 +344,8 @@ int main() {
   const Tensors t{{ten[0], ten[1], ten[2], ten[3], ten[4], ten[5]}, ten[6]};
   if (!layout_pattern<false, 32, 64, 64, true>(b, t, 64, "gdn_headline")) return 1;
   if (!layout_pattern<false, 16, 512, 96, false>(b, t, 32, "gdn_config4")) return 1;
+  // config 4's pattern with the o stores non-temporal (the kernel stores them through L2)
+  if (!layout_pattern<false, 16, 512, 96, true>(b, t, 32, "gdn_c4_nt")) return 1;
   if (!layout_pattern<true, 32, 128, 96, true>(b, t, 64, "kda_config5")) return 1;
   for (int i = 0; i < 7; ++i) (void)hipFree(ten[i]);
   (void)hipFree(b.src);
