@@ -10,15 +10,18 @@
 //   S   <- diag(e^{G_last}) S + (k e^{G_last - G})^T v_new
 //
 // Stage 1 (kda_local_kernel, one workgroup per chunk) does everything that does not depend on S:
-// the cumsum, the gated operands, A, the inverse, W, U and the score P; it writes W, U,
-// QE = scale q e^G, KR = k e^{G_last - G}, P = causal_incl(QE b^T) (bf16) and the chunk decay
-// e^{G_last} (fp32).  Stage 2 (kda_scan_split_kernel, pf_kda_scan.h, one workgroup per (chain,
-// 32-column slice)) carries S in registers through the chain:
+// the cumsum, the gated operands, A, the inverse, W and the score P; it writes W,
+// TB = T diag(beta), QE = scale q e^G, KR = k e^{G_last - G}, P = causal_incl(QE b^T) (bf16) and
+// the chunk decay e^{G_last} (fp32).  Stage 2 (kda_scan_split_kernel, pf_kda_scan.h, one
+// workgroup per (chain, 32-column slice)) carries S in registers through the chain:
 //
-//   Y = W S,  v_new = U - Y,  o^T = v_new^T P^T + (QE S)^T,  S <- e^{G_last} (.) S + KR^T v_new
+//   U = TB v,  Y = W S,  v_new = U - Y,  o^T = v_new^T P^T + (QE S)^T,
+//   S <- e^{G_last} (.) S + KR^T v_new
 //
 // so its chunk images hold the already-gated operands and the per-channel decay is one multiply
-// of the state rows per chunk.
+// of the state rows per chunk.  U is formed in stage 2 from v and the 64 x 64 TB rather than
+// written by stage 1: stage 1 then reads no v, and TB (8 KiB per chunk) replaces U (16 KiB) on
+// the way through HBM.
 #pragma once
 
 #include "pf_chunk_local.h"
@@ -31,12 +34,11 @@ namespace pf {
 struct KdaLocalArgs {
   const bf16* q;        // [M*C, DK]
   const bf16* k;        // [M*C, DK]
-  const bf16* v;        // [M*C, DV]
   const float* g;       // [M*C, DK] per-token, per-channel log decay (cumsummed here)
   const float* beta;    // [M*C]
   float scale;
   bf16* W;              // [M, C, DK]  T diag(beta) (k e^G)
-  bf16* U;              // [M, C, DV]  T diag(beta) v
+  bf16* TB;             // [M, C, C]   T diag(beta), zeros above the diagonal
   bf16* QE;             // [M*C, DK]   scale q e^G
   bf16* KR;             // [M*C, DK]   k e^{G_last - G}
   bf16* P;              // [M, C, C]   causal_incl(QE (k e^-G)^T); upper blocks (0,1), (2,3) zero
@@ -45,7 +47,7 @@ struct KdaLocalArgs {
 
 // Row tiles of stage 1 use the swizzle of the stage-2 k tile: element (r, col) lives at
 // r*KP + 4*((col/4) ^ ((r >> 2) & 3)) + col%4 with KP = DK + 16, so both the row reads of the score
-// products and the transposed reads of the W/U products are free of bank conflicts.
+// products and the transposed reads of the W products are free of bank conflicts.
 template <int KP>
 __device__ __forceinline__ int kda_swz(int r, int col) {
   return r * KP + 4 * ((col >> 2) ^ ((r >> 2) & 3)) + (col & 3);
@@ -106,8 +108,7 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   // LDS regions, by phase:
   //   [0, 3 TILE) bf16 : tiles a | b | qe   (the fp32 g staging [C][DK] aliases the start)
   //   [3 TILE, ..) fp32: A [C][CP]
-  // after the scores: T (fp32) takes the qe tile, the v tile takes the b tile, T diag(beta)
-  // (bf16) takes A.
+  // after the scores: T (fp32) takes the qe tile, T diag(beta) (bf16) takes A.
   static_assert(C * CP * 4 <= TILE * 2 && C * DK * 4 <= 3 * TILE * 2 && C * TPB * 2 <= C * CP * 4, "LDS aliasing");
   __shared__ __attribute__((aligned(16))) bf16 tiles[3 * TILE];
   __shared__ __attribute__((aligned(16))) float As[C * CP];
@@ -117,7 +118,6 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   bf16* qt = tiles + 2 * TILE;
   float* gsm = reinterpret_cast<float*>(tiles);
   float* Ts = reinterpret_cast<float*>(qt);
-  bf16* vt = bt;
   bf16* Tb = reinterpret_cast<bf16*>(As);
 
   const int m = blockIdx.x;
@@ -127,13 +127,12 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   const int rb = tid >> 4, vc = (tid & 15) * 8;
 
   // ---- 1. loads; g to LDS ----------------------------------------------------------------
-  uint4 kr[4], qr[4], vr[4];
+  uint4 kr[4], qr[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const size_t e = (row0 + rb + 16 * i) * DK + vc;
     kr[i] = *reinterpret_cast<const uint4*>(a.k + e);
     qr[i] = *reinterpret_cast<const uint4*>(a.q + e);
-    vr[i] = *reinterpret_cast<const uint4*>(a.v + (row0 + rb + 16 * i) * DV + vc);
     const floatx4 g0 = *reinterpret_cast<const floatx4*>(a.g + e);
     const floatx4 g1 = *reinterpret_cast<const floatx4*>(a.g + e + 4);
     *reinterpret_cast<floatx4*>(gsm + (rb + 16 * i) * DK + vc) = g0;
@@ -224,7 +223,7 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   // ---- 5. T = (I + A)^-1 (fp32) ------------------------------------------------------------
   unit_lower_inverse64(As, Ts);
 
-  // ---- 6. T diag(beta) as bf16 (in A's space), the v tile (in b's space) -------------------
+  // ---- 6. T diag(beta) as bf16 (in A's space) ----------------------------------------------
   for (int u = tid; u < C * C / 4; u += 256) {
     const int i = u / (C / 4), j0 = (u % (C / 4)) * 4;
     const floatx4 t4 = *reinterpret_cast<const floatx4*>(Ts + i * CP + j0);
@@ -232,29 +231,26 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
     store4(Tb + i * TPB + j0, (j0 <= i) ? t4[0] * b4[0] : 0.f, (j0 + 1 <= i) ? t4[1] * b4[1] : 0.f,
            (j0 + 2 <= i) ? t4[2] * b4[2] : 0.f, (j0 + 3 <= i) ? t4[3] * b4[3] : 0.f);
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = rb + 16 * i;
-    const bf16x8 vx = __builtin_bit_cast(bf16x8, vr[i]);
-    *reinterpret_cast<bf16x4*>(vt + kda_swz<KP>(r, vc)) = bf16x4{vx[0], vx[1], vx[2], vx[3]};
-    *reinterpret_cast<bf16x4*>(vt + kda_swz<KP>(r, vc + 4)) = bf16x4{vx[4], vx[5], vx[6], vx[7]};
-  }
   lds_barrier();
+  // TB to HBM for stage 2: thread tid writes row tid / 4, columns 16 (tid % 4) .. +15
+  {
+    const int i = tid >> 2, j0 = 16 * (tid & 3);
+    bf16* dst = a.TB + ((size_t)m * C + i) * C + j0;
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(Tb + i * TPB + j0);
+    *reinterpret_cast<uint4*>(dst + 8) = *reinterpret_cast<const uint4*>(Tb + i * TPB + j0 + 8);
+  }
 
-  // ---- 7. W^T = a^T (T diag beta)^T, U^T = v^T (T diag beta)^T ------------------------------
-  // Wave w owns the 16-row blocks mb = 2w, 2w+1 of the dk (dv) dimension.  A operand: a^T / v^T
-  // by transpose reads (lane (c,g) gets rows j = 32kb + 4g + 0..3 and +16 of column 16mb + c);
+  // ---- 7. W^T = a^T (T diag beta)^T ---------------------------------------------------------
+  // Wave w owns the 16-row blocks mb = 2w, 2w+1 of the dk dimension.  A operand: a^T by
+  // transpose reads (lane (c,g) gets rows j = 32kb + 4g + 0..3 and +16 of column 16mb + c);
   // B operand: rows i = 16nb + c of T diag(beta) at the same (permuted) j.  The D registers hold
   // W[i][16mb + 4g .. +3]: four consecutive columns, one 8-byte store.
   {
-    floatx4 accW[2][4], accU[2][4];
+    floatx4 accW[2][4];
 #pragma unroll
     for (int mb2 = 0; mb2 < 2; ++mb2)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        accW[mb2][nb] = zero4();
-        accU[mb2][nb] = zero4();
-      }
+      for (int nb = 0; nb < 4; ++nb) accW[mb2][nb] = zero4();
     const int tr = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g);     // transposed reads
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
@@ -266,9 +262,7 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
         for (int mb2 = 0; mb2 < 2; ++mb2) {
           const int mb = 2 * w + mb2;
           const bf16* ap = at + 32 * kb * KP + tr + 16 * mb;
-          const bf16* vp = vt + 32 * kb * KP + tr + 16 * mb;
           accW[mb2][nb] = mfma_bf16(cat8(lds_read_tr(ap), lds_read_tr(ap + 16 * KP)), tbv, accW[mb2][nb]);
-          accU[mb2][nb] = mfma_bf16(cat8(lds_read_tr(vp), lds_read_tr(vp + 16 * KP)), tbv, accU[mb2][nb]);
         }
       }
     }
@@ -277,9 +271,8 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const size_t e = ((size_t)m * C + 16 * nb + c) * DK + 16 * (2 * w + mb2) + 4 * g;
-        const floatx4 x = accW[mb2][nb], y = accU[mb2][nb];
+        const floatx4 x = accW[mb2][nb];
         store4(a.W + e, x[0], x[1], x[2], x[3]);
-        store4(a.U + e, y[0], y[1], y[2], y[3]);
       }
   }
 }
@@ -288,7 +281,8 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
 
 struct KdaScanArgs {
   const bf16* W;        // [BH*NC, C, DK]
-  const bf16* U;        // [BH*NC, C, DV]
+  const bf16* TB;       // [BH*NC, C, C]   T diag(beta)
+  const bf16* v;        // [BH*T, DV]
   const bf16* QE;       // [BH*T, DK]
   const bf16* KR;       // [BH*T, DK]
   const bf16* P;        // [BH*NC, C, C]

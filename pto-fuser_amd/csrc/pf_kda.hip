@@ -20,6 +20,7 @@ using KdaWorkspace = pf::Workspace;
 
 // Byte layout of the KDA workspace, M = B*H*T/C chunks, E the operand type (bf16 or fp32):
 //   [ W | U | QE | KR  (each M*C*128 E) | P (M*C*C E) | DEC (M*128 fp32) ]
+// (bf16 operands keep T diag(beta), M*C*C bf16, in U's place: their stage 2 forms U itself.)
 struct KdaLayout {
   size_t w_off, u_off, q_off, k_off, p_off, d_off, total;
   KdaLayout(size_t M, int C, int D, int dtype) {
@@ -122,12 +123,11 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   pf::KdaLocalArgs la{};
   la.q = static_cast<const bf16*>(q);
   la.k = static_cast<const bf16*>(k);
-  la.v = static_cast<const bf16*>(v);
   la.g = g;
   la.beta = beta;
   la.scale = scale;
   la.W = reinterpret_cast<bf16*>(base + lay.w_off);
-  la.U = reinterpret_cast<bf16*>(base + lay.u_off);
+  la.TB = reinterpret_cast<bf16*>(base + lay.u_off);
   la.QE = reinterpret_cast<bf16*>(base + lay.q_off);
   la.KR = reinterpret_cast<bf16*>(base + lay.k_off);
   la.P = reinterpret_cast<bf16*>(base + lay.p_off);
@@ -139,7 +139,8 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
 
   pf::KdaScanArgs sa{};
   sa.W = la.W;
-  sa.U = la.U;
+  sa.TB = la.TB;
+  sa.v = static_cast<const bf16*>(v);
   sa.QE = la.QE;
   sa.KR = la.KR;
   sa.P = la.P;

@@ -4,10 +4,13 @@
 //
 // Workgroup = one chain bh x one slice of 32 state columns (NT = 2 column tiles of 16).  Stage 1
 // (kda_local_kernel) leaves per chunk the gated images W = T diag(beta) (k e^G),
-// U = T diag(beta) v, QE = scale q e^G, KR = k e^{G_last - G}, P = causal_incl(QE (k e^-G)^T) and
+// TB = T diag(beta), QE = scale q e^G, KR = k e^{G_last - G}, P = causal_incl(QE (k e^-G)^T) and
 // the chunk decay e^{G_last} per key channel, so the recurrence needs no T r step:
 //
-//   Y = W S,  v_new = U - Y,  o = QE S + P v_new,  S <- e^{G_last} (.) S + KR^T v_new.
+//   U = TB v,  Y = W S,  v_new = U - Y,  o = QE S + P v_new,  S <- e^{G_last} (.) S + KR^T v_new.
+//
+// U does not depend on the state: each wave forms its 16 rows (TB's rows of its tokens against
+// the slice's v tile, 2 or 4 products) beside Y.
 //
 // Compute wave w owns tokens 16w..16w+15 of every chunk (its rows of Y, v_new and o) and state
 // rows 32w..32w+31 (fp32, MFMA D layout, in registers for the whole chain).  The two products
@@ -21,20 +24,21 @@
 //       w >> 1; it is the A operand of o^T = v_new^T P^T (causal: blocks 0..w>>1) and the B
 //       operand of the state update (both blocks).
 //
-//   phase 1  Y = W S~, (QE S~)^T, v_new = U - Y -> VX                                      B1
+//   phase 1  U = TB v, Y = W S~, (QE S~)^T, v_new = U - Y -> VX                            B1
 //   phase 2  o^T = v_new^T P^T + (QE S~)^T -> HBM; S~ <- e^{G_last} (.) S~ + KR^T VX -> SB   B2
 //
 // SB is read in phase 1 and written in phase 2, VX the other way round, so one copy of each
-// suffices.  Per wave and chunk: 8 products for W S, 8 for (QE S)^T, 2 or 4 for P v_new and 8
-// for the update.  The per-channel decay is one multiply of the 32 state values a lane holds.
+// suffices.  Per wave and chunk: 2 or 4 products for U, 8 for W S, 8 for (QE S)^T, 2 or 4 for
+// P v_new and 8 for the update.  The per-channel decay is one multiply of the 32 state values a lane holds.
 //
 // Four loader waves own the loads: chunk c+3's loads issued while the compute waves work on chunk
 // c (three rotating register sets), chunk c+1 written into the free half of a double-buffered LDS
 // stage (W, QE, KR rows swizzled for the permuted-K operand reads and the transposed KR^T reads,
-// P rows, the U tile row-major, the decay), W, P, U and the decay in the first phase, QE and KR
-// in the second.  The compute waves store their o rows themselves: two 16-byte stores per lane,
-// non-temporal, after lanes c and c + 8 swap the halves of a token's 128-byte row so that every
-// store instruction writes whole lines.
+// P rows, the v tile row-major, the decay), W, P, v and the decay in the first phase, QE and KR
+// in the second.  TB has one LDS copy: it is read only in phase 1, so chunk c+1's TB (loaded with
+// P) is written in the second phase of interval c.  The compute waves store their o rows
+// themselves: two 16-byte stores per lane, non-temporal, after lanes c and c + 8 swap the halves
+// of a token's 128-byte row so that every store instruction writes whole lines.
 #pragma once
 
 #include "pf_gfx950.h"
@@ -47,22 +51,22 @@ template <int C, int DK, int NCOL>
 struct KdaSplitStage {
   static constexpr int KP = DK + 16;   // W, QE, KR rows: Swz<2,3>
   static constexpr int TP = C + 8;     // P rows: Swz<3,1>
-  static constexpr int UP = NCOL + 8;  // U tile rows (row-major, read transposed)
+  static constexpr int UP = NCOL + 8;  // v tile rows (row-major, read transposed)
   bf16 ws[C * KP];
   bf16 qs[C * KP];
   bf16 ks[C * KP];
   bf16 ps[C * TP];
-  bf16 us[C * UP];
+  bf16 vs[C * UP];
   float dec[DK];
 };
 
-// Loader register image of one chunk (W, QE, KR: 1024 16-byte vectors each; P: 512; U: 8 NCOL;
-// the decay: 32).
+// Loader register image of one chunk (W, QE, KR: 1024 16-byte vectors each; P, TB: 512 each;
+// v: 8 NCOL; the decay: 32).
 template <int NLW, int NCOL>
 struct KdaSplitRegs {
   static constexpr int NK = 1024 / (64 * NLW), NTR = 512 / (64 * NLW);
   static constexpr int NV = (8 * NCOL + 64 * NLW - 1) / (64 * NLW);
-  uint4 w[NK], q[NK], k[NK], p[NTR], u[NV];
+  uint4 w[NK], q[NK], k[NK], p[NTR], t[NTR], u[NV];
   uint4 d;
 };
 
@@ -79,6 +83,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
                 "tile shapes of the KDA split scan kernel: C 64, DK = DV 128, 32 columns");
 
   __shared__ __attribute__((aligned(16))) Stage st[2];
+  __shared__ __attribute__((aligned(16))) bf16 TBs[C * TP];        // TB of the current chunk
   __shared__ __attribute__((aligned(16))) bf16 SB[4 * NT * FRAG];
   __shared__ __attribute__((aligned(16))) bf16 VX[2 * NT * FRAG];
 
@@ -103,8 +108,9 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.W + (size_t)bh * Tlen * DK, Tlen * DK * 2);
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.QE + (size_t)bh * Tlen * DK, Tlen * DK * 2);
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.KR + (size_t)bh * Tlen * DK, Tlen * DK * 2);
-    const __amdgpu_buffer_rsrc_t ru = make_rsrc(a.U + (size_t)bh * Tlen * DV, Tlen * DV * 2);
+    const __amdgpu_buffer_rsrc_t ru = make_rsrc(a.v + (size_t)bh * Tlen * DV, Tlen * DV * 2);
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.P + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
+    const __amdgpu_buffer_rsrc_t rtb = make_rsrc(a.TB + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.DEC + (size_t)bh * NC * DK, (uint32_t)NC * DK * 4);
     // W / QE / KR rows (16 vectors of 8 per row): vec = lt & 15, a = lt >> 4; the vector index i
     // supplies the row bits that decide the swizzle's half swap, so the swap is compile-time:
@@ -114,15 +120,16 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     const uint32_t k_voff = (uint32_t)(krow_l * DK + kvec * 8) * 2;
     const int k_lds = krow_l * KP + 8 * (kvec ^ ((ka >> 2) & 1));   // Swz<2,3>: slot ^= row bit 3
     auto krow_i = [](int i) -> int { return ((i & 1) << 2) | (((i >> 1) & 1) << 5); };
-    // P rows (8 vectors per row): vec = lt & 7, a = lt >> 3; row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | a4<<5
+    // P and TB rows (8 vectors per row): vec = lt & 7, a = lt >> 3;
+    // row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | a4<<5
     const int ta = lt >> 3, tvec = lt & 7;
     const int prow_l = (ta & 7) | ((ta >> 3) << 4);
     const uint32_t p_voff = (uint32_t)(prow_l * C + tvec * 8) * 2;
     const int p_lds = prow_l * TP + 8 * tvec;
     auto prow_i = [](int i) -> int { return (i & 1) << 3; };
-    // U tile (NCOL / 8 vectors per row): vector u = lt + 64 NLW i
+    // v tile (NCOL / 8 vectors per row): vector u = lt + 64 NLW i
     constexpr int VPR = NCOL / 8, VSTEP = 64 * NLW / VPR;
-    static_assert(C * VPR == 64 * NLW * Regs::NV, "the U tile divides over the loader lanes");
+    static_assert(C * VPR == 64 * NLW * Regs::NV, "the v tile divides over the loader lanes");
     const int urow_l = lt / VPR, uvec = lt % VPR;
     const uint32_t u_voff = (uint32_t)(urow_l * DV + col0 + uvec * 8) * 2;
     // decay: 32 vectors of 4 floats (lanes 32.. repeat lanes 0..31: no branch around a load)
@@ -143,7 +150,10 @@ void kda_scan_split_kernel(KdaScanArgs a) {
       for (int i = 0; i < Regs::NK; ++i) r.k[i] = buf_load16(rk, k_voff, k_s + krow_i(i) * DK * 2);
       const uint32_t p_s = (uint32_t)ch * C * C * 2;
 #pragma unroll
-      for (int i = 0; i < Regs::NTR; ++i) r.p[i] = buf_load16(rp, p_voff, p_s + prow_i(i) * C * 2);
+      for (int i = 0; i < Regs::NTR; ++i) {
+        r.p[i] = buf_load16(rp, p_voff, p_s + prow_i(i) * C * 2);
+        r.t[i] = buf_load16(rtb, p_voff, p_s + prow_i(i) * C * 2);
+      }
       const uint32_t u_s = (uint32_t)ch * C * DV * 2;
 #pragma unroll
       for (int i = 0; i < Regs::NV; ++i) r.u[i] = buf_load16(ru, u_voff, u_s + (uint32_t)(VSTEP * i) * DV * 2);
@@ -156,7 +166,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
       for (int i = 0; i < Regs::NTR; ++i) put16(s.ps + p_lds + prow_i(i) * TP, r.p[i], (i & 1) != 0);
 #pragma unroll
       for (int i = 0; i < Regs::NV; ++i)
-        *reinterpret_cast<uint4*>(s.us + (urow_l + VSTEP * i) * UP + uvec * 8) = r.u[i];
+        *reinterpret_cast<uint4*>(s.vs + (urow_l + VSTEP * i) * UP + uvec * 8) = r.u[i];
       if (lt < 32) *reinterpret_cast<uint4*>(s.dec + 4 * lt) = r.d;
     };
     auto store_qk = [&](Stage& s, const Regs& r) {
@@ -165,6 +175,10 @@ void kda_scan_split_kernel(KdaScanArgs a) {
         put16(s.qs + k_lds + krow_i(i) * KP, r.q[i], (i & 1) != 0);
         put16(s.ks + k_lds + krow_i(i) * KP, r.k[i], (i & 1) != 0);
       }
+    };
+    auto store_tb = [&](const Regs& r) {
+#pragma unroll
+      for (int i = 0; i < Regs::NTR; ++i) put16(TBs + p_lds + prow_i(i) * TP, r.t[i], (i & 1) != 0);
     };
 
     // Interval j (the compute waves work on chunk j from stage j & 1): chunk j+3's loads go into
@@ -182,6 +196,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
       lds_barrier();                                     // B1
       load_kpud(ld, nl);
       store_qk(sn, nx);
+      store_tb(nx);                                      // chunk j's TB was read before B1
       lds_barrier();                                     // B2
     };
     load_wq(r0, 0);
@@ -192,6 +207,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     load_kpud(r2, min(2, last));
     store_wpud(st[0], r0);
     store_qk(st[0], r0);
+    store_tb(r0);
     lds_barrier();                                       // start: stage 0 and SB ready
     if (NC > 1) {
       interval(r0, r1, 0);
@@ -215,8 +231,8 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     // per-lane LDS element offsets
     const int kq_rd = (tok0 + c) * KP + 4 * (g ^ ((c >> 2) & 3));          // W / QE rows
     const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g) + 32 * cw; // KR^T, rows 32cw..
-    const int p_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // P rows
-    const int u_rd = (tok0 + 4 * g + (c >> 2)) * UP + 4 * (c & 3);         // U, transposed read
+    const int p_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // P, TB rows
+    const int v_rd = (4 * g + (c >> 2)) * UP + 4 * (c & 3);                // v, transposed read
     const int frag = lane * 8;                                             // lane's exchange slot
     const int xhalf = 4 * (cw & 1), xblk = cw >> 1;                        // this wave's VX slot
 
@@ -238,7 +254,25 @@ void kda_scan_split_kernel(KdaScanArgs a) {
 
     for (int ch = 0; ch < NC; ++ch) {
       const Stage& s = st[ch & 1];
-      // ---- phase 1: Y = W S~, (QE S~)^T for this wave's 16 tokens, v_new = U - Y -> VX ----
+      // ---- phase 1: U = TB v, Y = W S~, (QE S~)^T for this wave's 16 tokens, v_new = U - Y -> VX
+      // U's products: A = TB rows of the wave's tokens (lower triangular: key blocks 0..cw>>1),
+      // B = the v tile read transposed (lane (c, g): tokens 32 kb + 4 g + 0..3 and + 16,
+      // column 16 nt + c), so lane (c, g) gets U[tok0 + 4 g + i][16 nt + c] like Y
+      floatx4 U[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) U[nt] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        if (kb == 0 || cw >= 2) {
+          const bf16* tp = TBs + p_rd + 32 * kb;
+          const bf16x8 ta = cat8(*reinterpret_cast<const bf16x4*>(tp), *reinterpret_cast<const bf16x4*>(tp + 16));
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const bf16* vp = s.vs + v_rd + 32 * kb * UP + 16 * nt;
+            U[nt] = mfma_bf16(ta, cat8(lds_read_tr(vp), lds_read_tr(vp + 16 * UP)), U[nt]);
+          }
+        }
+      }
       floatx4 Y[NT], QT[NT];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) { Y[nt] = zero4(); QT[nt] = zero4(); }
@@ -257,10 +291,9 @@ void kda_scan_split_kernel(KdaScanArgs a) {
       }
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const bf16x4 u4 = lds_read_tr(s.us + u_rd + 16 * nt);
         bf16x4 vb;
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) vb[ii] = (bf16)((float)u4[ii] - Y[nt][ii]);
+        for (int ii = 0; ii < 4; ++ii) vb[ii] = (bf16)(U[nt][ii] - Y[nt][ii]);
         *reinterpret_cast<bf16x4*>(VX + (xblk * NT + nt) * FRAG + frag + xhalf) = vb;
       }
       lds_barrier();                                     // B1
