@@ -276,15 +276,13 @@ LONG_WORKLOAD = dict(B=1, H=32, T=32768, C=64, DK=128, DV=128)
 
 def kda_model(B, H, T, C, DK, DV):
     """Algorithmic HBM bytes of the fused KDA forward per chunk of C tokens (bf16 operands):
-    stage 1 reads q, k (bf16), g (fp32 per channel), beta and writes W, QE, KR (bf16),
-    T diag(beta) (bf16, C x C), P (bf16: the lower 16x16 blocks and the two upper ones stage 2
-    reads), the chunk decay (fp32); stage 2 reads W, QE, KR, T diag(beta), P (whole), v, the decay
-    and writes o (fp32).  ``compulsory`` is what any forward must move: q, k, v, g, beta in, o
-    out."""
+    stage 1 reads q, k (bf16), g (fp32 per channel), beta and writes W, QE, KB (bf16),
+    T diag(beta) (bf16, C x C), the chunk decay (fp32); stage 2 reads W, QE, KB, T diag(beta), v,
+    the decay and writes o (fp32) (the causal score is formed on the chip).  ``compulsory`` is
+    what any forward must move: q, k, v, g, beta in, o out."""
     M = B * H * (T // C)
-    p_blocks = (C // 16) * (C // 16 + 1) // 2 + 2           # lower blocks + (0,1), (2,3)
-    s1 = 2 * C * DK * 2 + C * DK * 4 + C * 4 + 3 * C * DK * 2 + C * C * 2 + p_blocks * 256 * 2 + DK * 4
-    s2 = 3 * C * DK * 2 + 2 * C * C * 2 + C * DV * 2 + DK * 4 + C * DV * 4
+    s1 = 2 * C * DK * 2 + C * DK * 4 + C * 4 + 3 * C * DK * 2 + C * C * 2 + DK * 4
+    s2 = 3 * C * DK * 2 + C * C * 2 + C * DV * 2 + DK * 4 + C * DV * 4
     final = B * H * DK * DV * 4
     compulsory = M * (3 * C * DK * 2 + C * DK * 4 + C * 4 + C * DV * 4) + final
     return {"units": M, "bytes_per_unit": s1 + s2, "bytes": M * (s1 + s2) + final,

@@ -7,21 +7,21 @@
 //   W    = T diag(beta) a,   U = T diag(beta) v           (the WY form)
 //   v_new = U - W S
 //   o    = scale (q e^G) S + scale causal_incl((q e^G) b^T) v_new
-//   S   <- diag(e^{G_last}) S + (k e^{G_last - G})^T v_new
+//   S   <- diag(e^{G_last}) (S + b^T v_new)     (= diag(e^{G_last}) S + (k e^{G_last - G})^T v_new)
 //
-// Stage 1 (kda_local_kernel, one workgroup per chunk) does everything that does not depend on S:
-// the cumsum, the gated operands, A, the inverse, W and the score P; it writes W,
-// TB = T diag(beta), QE = scale q e^G, KR = k e^{G_last - G}, P = causal_incl(QE b^T) (bf16) and
-// the chunk decay e^{G_last} (fp32).  Stage 2 (kda_scan_split_kernel, pf_kda_scan.h, one
-// workgroup per (chain, 32-column slice)) carries S in registers through the chain:
+// Stage 1 (kda_local_kernel, one workgroup per chunk) does what needs the whole chunk's gates at
+// once: the cumsum, the gated operands, A and the inverse; it writes W, TB = T diag(beta),
+// QE = scale q e^G, KB = b (bf16) and the chunk decay e^{G_last} (fp32).  Stage 2
+// (kda_scan_split_kernel, pf_kda_scan.h, one workgroup per (chain, 32-column slice)) carries S in
+// registers through the chain:
 //
-//   U = TB v,  Y = W S,  v_new = U - Y,  o^T = v_new^T P^T + (QE S)^T,
-//   S <- e^{G_last} (.) S + KR^T v_new
+//   U = TB v,  P = causal_incl(QE KB^T),  Y = W S,  v_new = U - Y,
+//   o^T = v_new^T P^T + (QE S)^T,  S <- e^{G_last} (.) (S + KB^T v_new)
 //
 // so its chunk images hold the already-gated operands and the per-channel decay is one multiply
-// of the state rows per chunk.  U is formed in stage 2 from v and the 64 x 64 TB rather than
-// written by stage 1: stage 1 then reads no v, and TB (8 KiB per chunk) replaces U (16 KiB) on
-// the way through HBM.
+// of the state rows per chunk.  U and the score are formed in stage 2 from what it stages anyway
+// (v, QE, KB) rather than written by stage 1: stage 1 then reads no v and writes neither U
+// (16 KiB per chunk) nor P (6 KiB), only the 64 x 64 TB (8 KiB).
 #pragma once
 
 #include "pf_chunk_local.h"
@@ -40,25 +40,23 @@ struct KdaLocalArgs {
   bf16* W;              // [M, C, DK]  T diag(beta) (k e^G)
   bf16* TB;             // [M, C, C]   T diag(beta), zeros above the diagonal
   bf16* QE;             // [M*C, DK]   scale q e^G
-  bf16* KR;             // [M*C, DK]   k e^{G_last - G}
-  bf16* P;              // [M, C, C]   causal_incl(QE (k e^-G)^T); upper blocks (0,1), (2,3) zero
+  bf16* KB;             // [M*C, DK]   k e^-G
   float* DEC;           // [M, DK]     e^{G_last}
 };
 
 // Row tiles of stage 1 use the swizzle of the stage-2 k tile: element (r, col) lives at
-// r*KP + 4*((col/4) ^ ((r >> 2) & 3)) + col%4 with KP = DK + 16, so both the row reads of the score
+// r*KP + 4*((col/4) ^ ((r >> 2) & 3)) + col%4 with KP = DK + 16, so both the row reads of the A
 // products and the transposed reads of the W products are free of bank conflicts.
 template <int KP>
 __device__ __forceinline__ int kda_swz(int r, int col) {
   return r * KP + 4 * ((col >> 2) ^ ((r >> 2) & 3)) + (col & 3);
 }
 
-// One wave's score blocks of the KDA chunk (the GDN kernel's lists, score_code): products over
-// the swizzled a / b / qe tiles, then the mask epilogue (A scaled by beta_i into LDS, P to global).
+// One wave's blocks of A for the KDA chunk (the GDN kernel's A lists, score_code): products over
+// the swizzled a / b tiles, then the mask epilogue (A scaled by beta_i into LDS).
 template <int C, int KP, int CP, int W>
-__device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, const bf16* qt, float* As,
-                                               const float* Bs, bf16* P) {
-  constexpr int N = score_count(kScoreAP, W);
+__device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, float* As, const float* Bs) {
+  constexpr int N = score_count(kScoreA, W);
   const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int rd = c * KP + 4 * (g ^ ((c >> 2) & 3));   // row c, K groups g and g+4 of each 32-block
   floatx4 acc[N];
@@ -68,9 +66,9 @@ __device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, c
   for (int kb = 0; kb < 128 / 32; ++kb) {
 #pragma unroll
     for (int b = 0; b < N; ++b) {
-      const int code = score_code(kScoreAP, W, b);
+      const int code = score_code(kScoreA, W, b);
       const bf16* jp = bt + 16 * (code & 3) * KP + rd + 32 * kb;
-      const bf16* ip = ((code & 16) ? qt : at) + 16 * ((code >> 2) & 3) * KP + rd + 32 * kb;
+      const bf16* ip = at + 16 * ((code >> 2) & 3) * KP + rd + 32 * kb;
       const bf16x8 ja = cat8(*reinterpret_cast<const bf16x4*>(jp), *reinterpret_cast<const bf16x4*>(jp + 16));
       const bf16x8 ib = cat8(*reinterpret_cast<const bf16x4*>(ip), *reinterpret_cast<const bf16x4*>(ip + 16));
       acc[b] = mfma_bf16(ja, ib, acc[b]);   // equal rows: one LDS read
@@ -78,23 +76,13 @@ __device__ __forceinline__ void kda_score_wave(const bf16* at, const bf16* bt, c
   }
 #pragma unroll
   for (int b = 0; b < N; ++b) {
-    const int code = score_code(kScoreAP, W, b);
+    const int code = score_code(kScoreA, W, b);
     const int i = 16 * ((code >> 2) & 3) + c, j0 = 16 * (code & 3) + 4 * g;
     floatx4 out;
-    if (!(code & 16)) {
-      const float bi = Bs[i];
+    const float bi = Bs[i];
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) out[ii] = (i > j0 + ii) ? bi * acc[b][ii] : 0.f;
-      *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
-    } else {
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) out[ii] = (i >= j0 + ii) ? acc[b][ii] : 0.f;
-      store4(P + i * C + j0, out[0], out[1], out[2], out[3]);
-    }
-  }
-  if (W == 0 || W == 3) {   // the upper blocks (0,1) and (2,3) the scan reads; see score_wave
-    const int i = (W == 0 ? 0 : 32) + c, j0 = (W == 0 ? 16 : 48) + 4 * g;
-    store4(P + i * C + j0, 0.f, 0.f, 0.f, 0.f);
+    for (int ii = 0; ii < 4; ++ii) out[ii] = (i > j0 + ii) ? bi * acc[b][ii] : 0.f;
+    *reinterpret_cast<floatx4*>(As + i * CP + j0) = out;
   }
 }
 
@@ -106,18 +94,17 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   constexpr int TPB = C + 8;           // bf16 T diag(beta)
   constexpr int TILE = C * KP;         // elements of one row tile
   // LDS regions, by phase:
-  //   [0, 3 TILE) bf16 : tiles a | b | qe   (the fp32 g staging [C][DK] aliases the start)
+  //   [0, 3 TILE) bf16 : tiles a | b | (spare)   (the fp32 g staging [C][DK] aliases the start)
   //   [3 TILE, ..) fp32: A [C][CP]
-  // after the scores: T (fp32) takes the qe tile, T diag(beta) (bf16) takes A.
+  // after the products of A: T (fp32) takes the third tile, T diag(beta) (bf16) takes A.
   static_assert(C * CP * 4 <= TILE * 2 && C * DK * 4 <= 3 * TILE * 2 && C * TPB * 2 <= C * CP * 4, "LDS aliasing");
   __shared__ __attribute__((aligned(16))) bf16 tiles[3 * TILE];
   __shared__ __attribute__((aligned(16))) float As[C * CP];
   __shared__ __attribute__((aligned(16))) float Bs[C];
   bf16* at = tiles;
   bf16* bt = tiles + TILE;
-  bf16* qt = tiles + 2 * TILE;
   float* gsm = reinterpret_cast<float*>(tiles);
-  float* Ts = reinterpret_cast<float*>(qt);
+  float* Ts = reinterpret_cast<float*>(tiles + 2 * TILE);
   bf16* Tb = reinterpret_cast<bf16*>(As);
 
   const int m = blockIdx.x;
@@ -183,7 +170,7 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   for (int i = 0; i < 4; ++i) {
     const int r = rb + 16 * i;
     const bf16x8 kx = __builtin_bit_cast(bf16x8, kr[i]), qx = __builtin_bit_cast(bf16x8, qr[i]);
-    bf16x8 av, bv, qv, rv;
+    bf16x8 av, bv, qv;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float eg = __expf(G[i][e]), ebg = __expf(-G[i][e]);
@@ -191,32 +178,28 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
       av[e] = (bf16)(kf * eg);
       bv[e] = (bf16)(kf * ebg);
       qv[e] = (bf16)(a.scale * (float)qx[e] * eg);
-      rv[e] = (bf16)(kf * ebg * egl[e]);
     }
     const size_t e0 = (row0 + r) * DK + vc;
     *reinterpret_cast<bf16x8*>(a.QE + e0) = qv;
-    *reinterpret_cast<bf16x8*>(a.KR + e0) = rv;
+    *reinterpret_cast<bf16x8*>(a.KB + e0) = bv;
     // swizzled row tiles: two 4-element groups per vector
     const int o0 = kda_swz<KP>(r, vc), o1 = kda_swz<KP>(r, vc + 4);
     *reinterpret_cast<bf16x4*>(at + o0) = bf16x4{av[0], av[1], av[2], av[3]};
     *reinterpret_cast<bf16x4*>(at + o1) = bf16x4{av[4], av[5], av[6], av[7]};
     *reinterpret_cast<bf16x4*>(bt + o0) = bf16x4{bv[0], bv[1], bv[2], bv[3]};
     *reinterpret_cast<bf16x4*>(bt + o1) = bf16x4{bv[4], bv[5], bv[6], bv[7]};
-    *reinterpret_cast<bf16x4*>(qt + o0) = bf16x4{qv[0], qv[1], qv[2], qv[3]};
-    *reinterpret_cast<bf16x4*>(qt + o1) = bf16x4{qv[4], qv[5], qv[6], qv[7]};
   }
   lds_barrier();
 
-  // ---- 4. scores: A = beta_i (a b^T) strictly lower (fp32, LDS), P = causal_incl(qe b^T) --------
-  // The 20 lower 16x16 blocks are split over the waves as in the GDN chunk-local kernel (lists
-  // that share operand rows: b rows on the j side of every block, a rows for A and qe rows for
-  // P on the i side), each product formed transposed so a lane holds four consecutive columns
-  // of one score row.
+  // ---- 4. A = beta_i (a b^T) strictly lower (fp32, LDS) ------------------------------------
+  // The 10 lower 16x16 blocks are split over the waves as in the GDN chunk-local kernel (lists
+  // that share operand rows), each product formed transposed so a lane holds four consecutive
+  // columns of one row.
   switch (__builtin_amdgcn_readfirstlane(w)) {
-    case 0: kda_score_wave<C, KP, CP, 0>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
-    case 1: kda_score_wave<C, KP, CP, 1>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
-    case 2: kda_score_wave<C, KP, CP, 2>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
-    default: kda_score_wave<C, KP, CP, 3>(at, bt, qt, As, Bs, a.P + (size_t)m * C * C); break;
+    case 0: kda_score_wave<C, KP, CP, 0>(at, bt, As, Bs); break;
+    case 1: kda_score_wave<C, KP, CP, 1>(at, bt, As, Bs); break;
+    case 2: kda_score_wave<C, KP, CP, 2>(at, bt, As, Bs); break;
+    default: kda_score_wave<C, KP, CP, 3>(at, bt, As, Bs); break;
   }
   lds_barrier();
 
@@ -284,8 +267,7 @@ struct KdaScanArgs {
   const bf16* TB;       // [BH*NC, C, C]   T diag(beta)
   const bf16* v;        // [BH*T, DV]
   const bf16* QE;       // [BH*T, DK]
-  const bf16* KR;       // [BH*T, DK]
-  const bf16* P;        // [BH*NC, C, C]
+  const bf16* KB;       // [BH*T, DK]      k e^-G
   const float* DEC;     // [BH*NC, DK]
   const float* h0;      // [BH, DK, DV] or null
   float* o;             // [BH*T, DV]

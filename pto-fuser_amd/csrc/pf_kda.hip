@@ -18,20 +18,23 @@ constexpr size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 using KdaWorkspace = pf::Workspace;
 
-// Byte layout of the KDA workspace, M = B*H*T/C chunks, E the operand type (bf16 or fp32):
-//   [ W | U | QE | KR  (each M*C*128 E) | P (M*C*C E) | DEC (M*128 fp32) ]
-// (bf16 operands keep T diag(beta), M*C*C bf16, in U's place: their stage 2 forms U itself.)
+// Byte layout of the KDA workspace, M = B*H*T/C chunks:
+//   fp32 operands  [ W | U | QE | KR  (each M*C*128 fp32) | P (M*C*C fp32) | DEC (M*128 fp32) ]
+//   bf16 operands  [ W (M*C*128) | T diag(beta) (M*C*C) | QE | k e^-G (M*C*128 each) | DEC ]
+// (bf16 stage 2 forms U and the score itself: nothing in P's place.)
 struct KdaLayout {
   size_t w_off, u_off, q_off, k_off, p_off, d_off, total;
   KdaLayout(size_t M, int C, int D, int dtype) {
-    const size_t esize = dtype == PF_DTYPE_BF16 ? sizeof(bf16) : sizeof(float);
+    const bool b16 = dtype == PF_DTYPE_BF16;
+    const size_t esize = b16 ? sizeof(bf16) : sizeof(float);
     const size_t tile = align256(M * C * D * esize);
+    const size_t square = align256(M * C * C * esize);
     w_off = 0;
     u_off = w_off + tile;
-    q_off = u_off + tile;
+    q_off = u_off + (b16 ? square : tile);
     k_off = q_off + tile;
     p_off = k_off + tile;
-    d_off = p_off + align256(M * C * C * esize);
+    d_off = p_off + (b16 ? 0 : square);
     total = d_off + align256(M * D * sizeof(float));
   }
 };
@@ -129,8 +132,7 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   la.W = reinterpret_cast<bf16*>(base + lay.w_off);
   la.TB = reinterpret_cast<bf16*>(base + lay.u_off);
   la.QE = reinterpret_cast<bf16*>(base + lay.q_off);
-  la.KR = reinterpret_cast<bf16*>(base + lay.k_off);
-  la.P = reinterpret_cast<bf16*>(base + lay.p_off);
+  la.KB = reinterpret_cast<bf16*>(base + lay.k_off);
   la.DEC = reinterpret_cast<float*>(base + lay.d_off);
   pf::LaunchScope scope;
   pf::kda_local_kernel<KC, KD, KD><<<dim3((unsigned)M), dim3(256), 0, s>>>(la);
@@ -142,8 +144,7 @@ int pf_kda_exec(const void* q, const void* k, const void* v, const float* beta, 
   sa.TB = la.TB;
   sa.v = static_cast<const bf16*>(v);
   sa.QE = la.QE;
-  sa.KR = la.KR;
-  sa.P = la.P;
+  sa.KB = la.KB;
   sa.DEC = la.DEC;
   sa.h0 = h0;
   sa.o = o;

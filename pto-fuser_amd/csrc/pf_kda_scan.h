@@ -4,13 +4,17 @@
 //
 // Workgroup = one chain bh x one slice of 32 state columns (NT = 2 column tiles of 16).  Stage 1
 // (kda_local_kernel) leaves per chunk the gated images W = T diag(beta) (k e^G),
-// TB = T diag(beta), QE = scale q e^G, KR = k e^{G_last - G}, P = causal_incl(QE (k e^-G)^T) and
-// the chunk decay e^{G_last} per key channel, so the recurrence needs no T r step:
+// TB = T diag(beta), QE = scale q e^G, KB = k e^-G and the chunk decay e^{G_last} per key
+// channel, so the recurrence needs no T r step:
 //
-//   U = TB v,  Y = W S,  v_new = U - Y,  o = QE S + P v_new,  S <- e^{G_last} (.) S + KR^T v_new.
+//   U = TB v,  P = causal_incl(QE KB^T),  Y = W S,  v_new = U - Y,  o = QE S + P v_new,
+//   S <- e^{G_last} (.) (S + KB^T v_new).
 //
-// U does not depend on the state: each wave forms its 16 rows (TB's rows of its tokens against
-// the slice's v tile, 2 or 4 products) beside Y.
+// U and P do not depend on the state: each wave forms its 16 rows of U (TB's rows of its tokens
+// against the slice's v tile, 2 or 4 products) beside Y, and the ten 16 x 16 tiles of P are
+// spread three, three, two, two over the waves (each tile P^T = KB_jb QE_ib^T, a wave's own QE
+// rows from the registers of Y's phase), the tiles (2,0), (3,0) and (3,1) reaching their
+// owners through PX.  The gates are inside QE and KB, so the tiles need only the causal mask.
 //
 // Compute wave w owns tokens 16w..16w+15 of every chunk (its rows of Y, v_new and o) and state
 // rows 32w..32w+31 (fp32, MFMA D layout, in registers for the whole chain).  The two products
@@ -24,19 +28,19 @@
 //       w >> 1; it is the A operand of o^T = v_new^T P^T (causal: blocks 0..w>>1) and the B
 //       operand of the state update (both blocks).
 //
-//   phase 1  U = TB v, Y = W S~, (QE S~)^T, v_new = U - Y -> VX                            B1
-//   phase 2  o^T = v_new^T P^T + (QE S~)^T -> HBM; S~ <- e^{G_last} (.) S~ + KR^T VX -> SB   B2
+//   phase 1  U = TB v, Y = W S~, (QE S~)^T, v_new = U - Y -> VX; P's tiles                 B1
+//   phase 2  o^T = v_new^T P^T + (QE S~)^T -> HBM; S~ <- e^{G_last} (.) (S~ + KB^T VX) -> SB  B2
 //
 // SB is read in phase 1 and written in phase 2, VX the other way round, so one copy of each
-// suffices.  Per wave and chunk: 2 or 4 products for U, 8 for W S, 8 for (QE S)^T, 2 or 4 for
-// P v_new and 8 for the update.  The per-channel decay is one multiply of the 32 state values a lane holds.
+// suffices.  Per wave and chunk: 2 or 4 products for U, 8 for W S, 8 for (QE S)^T, 8 or 12 for
+// P's tiles, 2 or 4 for P v_new and 8 for the update.  The per-channel decay is one multiply of the 32 state values a lane holds.
 //
 // Four loader waves own the loads: chunk c+3's loads issued while the compute waves work on chunk
 // c (three rotating register sets), chunk c+1 written into the free half of a double-buffered LDS
-// stage (W, QE, KR rows swizzled for the permuted-K operand reads and the transposed KR^T reads,
-// P rows, the v tile row-major, the decay), W, P, v and the decay in the first phase, QE and KR
-// in the second.  TB has one LDS copy: it is read only in phase 1, so chunk c+1's TB (loaded with
-// P) is written in the second phase of interval c.  The compute waves store their o rows
+// stage (W, QE, KB rows swizzled for the permuted-K operand reads and the transposed KB^T reads,
+// the v tile row-major, the decay), W, v and the decay in the first phase, QE and KB in the
+// second.  TB has one LDS copy: it is read only in phase 1, so chunk c+1's TB is written in the
+// second phase of interval c.  The compute waves store their o rows
 // themselves: two 16-byte stores per lane, non-temporal, after lanes c and c + 8 swap the halves
 // of a token's 128-byte row so that every store instruction writes whole lines.
 #pragma once
@@ -49,24 +53,23 @@ namespace pf {
 // LDS image of one KDA chunk (C = 64, DK = 128, NCOL = 32 columns).
 template <int C, int DK, int NCOL>
 struct KdaSplitStage {
-  static constexpr int KP = DK + 16;   // W, QE, KR rows: Swz<2,3>
-  static constexpr int TP = C + 8;     // P rows: Swz<3,1>
+  static constexpr int KP = DK + 16;   // W, QE, KB rows: Swz<2,3>
+  static constexpr int TP = C + 8;     // TB rows (the single copy outside the stage): Swz<3,1>
   static constexpr int UP = NCOL + 8;  // v tile rows (row-major, read transposed)
   bf16 ws[C * KP];
   bf16 qs[C * KP];
   bf16 ks[C * KP];
-  bf16 ps[C * TP];
   bf16 vs[C * UP];
   float dec[DK];
 };
 
-// Loader register image of one chunk (W, QE, KR: 1024 16-byte vectors each; P, TB: 512 each;
-// v: 8 NCOL; the decay: 32).
+// Loader register image of one chunk (W, QE, KB: 1024 16-byte vectors each; TB: 512; v: 8 NCOL;
+// the decay: 32).
 template <int NLW, int NCOL>
 struct KdaSplitRegs {
   static constexpr int NK = 1024 / (64 * NLW), NTR = 512 / (64 * NLW);
   static constexpr int NV = (8 * NCOL + 64 * NLW - 1) / (64 * NLW);
-  uint4 w[NK], q[NK], k[NK], p[NTR], t[NTR], u[NV];
+  uint4 w[NK], q[NK], k[NK], t[NTR], u[NV];
   uint4 d;
 };
 
@@ -86,6 +89,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 TBs[C * TP];        // TB of the current chunk
   __shared__ __attribute__((aligned(16))) bf16 SB[4 * NT * FRAG];
   __shared__ __attribute__((aligned(16))) bf16 VX[2 * NT * FRAG];
+  __shared__ __attribute__((aligned(16))) bf16 PX[3 * 64 * 4];   // P tiles (2,0) (3,0) (3,1)
 
   int bh, slice;
   const int bid = blockIdx.x;
@@ -107,12 +111,11 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     const int lt = tid - 256;                            // 0 .. 64*NLW-1
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.W + (size_t)bh * Tlen * DK, Tlen * DK * 2);
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.QE + (size_t)bh * Tlen * DK, Tlen * DK * 2);
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.KR + (size_t)bh * Tlen * DK, Tlen * DK * 2);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.KB + (size_t)bh * Tlen * DK, Tlen * DK * 2);
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(a.v + (size_t)bh * Tlen * DV, Tlen * DV * 2);
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.P + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
     const __amdgpu_buffer_rsrc_t rtb = make_rsrc(a.TB + (size_t)bh * NC * C * C, (uint32_t)NC * C * C * 2);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.DEC + (size_t)bh * NC * DK, (uint32_t)NC * DK * 4);
-    // W / QE / KR rows (16 vectors of 8 per row): vec = lt & 15, a = lt >> 4; the vector index i
+    // W / QE / KB rows (16 vectors of 8 per row): vec = lt & 15, a = lt >> 4; the vector index i
     // supplies the row bits that decide the swizzle's half swap, so the swap is compile-time:
     // row = a0 | a1<<1 | i0<<2 | a2<<3 | a3<<4 | i1<<5
     const int ka = lt >> 4, kvec = lt & 15;
@@ -120,7 +123,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     const uint32_t k_voff = (uint32_t)(krow_l * DK + kvec * 8) * 2;
     const int k_lds = krow_l * KP + 8 * (kvec ^ ((ka >> 2) & 1));   // Swz<2,3>: slot ^= row bit 3
     auto krow_i = [](int i) -> int { return ((i & 1) << 2) | (((i >> 1) & 1) << 5); };
-    // P and TB rows (8 vectors per row): vec = lt & 7, a = lt >> 3;
+    // TB rows (8 vectors per row): vec = lt & 7, a = lt >> 3;
     // row = a0 | a1<<1 | a2<<2 | i0<<3 | a3<<4 | a4<<5
     const int ta = lt >> 3, tvec = lt & 7;
     const int prow_l = (ta & 7) | ((ta >> 3) << 4);
@@ -150,10 +153,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
       for (int i = 0; i < Regs::NK; ++i) r.k[i] = buf_load16(rk, k_voff, k_s + krow_i(i) * DK * 2);
       const uint32_t p_s = (uint32_t)ch * C * C * 2;
 #pragma unroll
-      for (int i = 0; i < Regs::NTR; ++i) {
-        r.p[i] = buf_load16(rp, p_voff, p_s + prow_i(i) * C * 2);
-        r.t[i] = buf_load16(rtb, p_voff, p_s + prow_i(i) * C * 2);
-      }
+      for (int i = 0; i < Regs::NTR; ++i) r.t[i] = buf_load16(rtb, p_voff, p_s + prow_i(i) * C * 2);
       const uint32_t u_s = (uint32_t)ch * C * DV * 2;
 #pragma unroll
       for (int i = 0; i < Regs::NV; ++i) r.u[i] = buf_load16(ru, u_voff, u_s + (uint32_t)(VSTEP * i) * DV * 2);
@@ -162,8 +162,6 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     auto store_wpud = [&](Stage& s, const Regs& r) {
 #pragma unroll
       for (int i = 0; i < Regs::NK; ++i) put16(s.ws + k_lds + krow_i(i) * KP, r.w[i], (i & 1) != 0);
-#pragma unroll
-      for (int i = 0; i < Regs::NTR; ++i) put16(s.ps + p_lds + prow_i(i) * TP, r.p[i], (i & 1) != 0);
 #pragma unroll
       for (int i = 0; i < Regs::NV; ++i)
         *reinterpret_cast<uint4*>(s.vs + (urow_l + VSTEP * i) * UP + uvec * 8) = r.u[i];
@@ -230,8 +228,9 @@ void kda_scan_split_kernel(KdaScanArgs a) {
     const int tok0 = 16 * cw;                            // this wave's token block
     // per-lane LDS element offsets
     const int kq_rd = (tok0 + c) * KP + 4 * (g ^ ((c >> 2) & 3));          // W / QE rows
-    const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g) + 32 * cw; // KR^T, rows 32cw..
-    const int p_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // P, TB rows
+    const int kt_rd = (4 * g + (c >> 2)) * KP + 4 * ((c & 3) ^ g) + 32 * cw; // KB^T, rows 32cw..
+    const int kj_rd = c * KP + 4 * (g ^ ((c >> 2) & 3));                   // KB / QE rows 16 b + c
+    const int p_rd = (tok0 + c) * TP + 4 * (g ^ (c >> 3));                // TB rows
     const int v_rd = (4 * g + (c >> 2)) * UP + 4 * (c & 3);                // v, transposed read
     const int frag = lane * 8;                                             // lane's exchange slot
     const int xhalf = 4 * (cw & 1), xblk = cw >> 1;                        // this wave's VX slot
@@ -274,6 +273,7 @@ void kda_scan_split_kernel(KdaScanArgs a) {
         }
       }
       floatx4 Y[NT], QT[NT];
+      bf16x8 qf[DK / 32];                                 // QE rows, kept for P's tiles
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) { Y[nt] = zero4(); QT[nt] = zero4(); }
 #pragma unroll
@@ -281,12 +281,12 @@ void kda_scan_split_kernel(KdaScanArgs a) {
         const bf16* wp = s.ws + kq_rd + 32 * kb;
         const bf16* qp = s.qs + kq_rd + 32 * kb;
         const bf16x8 wf = cat8(*reinterpret_cast<const bf16x4*>(wp), *reinterpret_cast<const bf16x4*>(wp + 16));
-        const bf16x8 qf = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+        qf[kb] = cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const bf16x8 sb = *reinterpret_cast<const bf16x8*>(SB + (kb * NT + nt) * FRAG + frag);
           Y[nt] = mfma_bf16(wf, sb, Y[nt]);               // (W S~)[t][n]
-          QT[nt] = mfma_bf16(sb, qf, QT[nt]);             // (QE S~)^T[n][t]
+          QT[nt] = mfma_bf16(sb, qf[kb], QT[nt]);         // (QE S~)^T[n][t]
         }
       }
 #pragma unroll
@@ -295,6 +295,46 @@ void kda_scan_split_kernel(KdaScanArgs a) {
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) vb[ii] = (bf16)(U[nt][ii] - Y[nt][ii]);
         *reinterpret_cast<bf16x4*>(VX + (xblk * NT + nt) * FRAG + frag + xhalf) = vb;
+      }
+      // P's tiles: tile (ib, jb) (query tokens 16 ib .., key tokens 16 jb .., jb <= ib) is
+      // P^T = KB_jb QE_ib^T, so lane (c, g) holds P[16 ib + c][16 jb + 4 g + i]; tiles (ib, 2 kb)
+      // and (ib, 2 kb + 1) together are the permuted-K B fragment of o^T = v_new^T P^T for key
+      // block kb.  Three, three, two and two tiles per wave; a wave's own QE rows come from qf.
+      bf16x4 ptl[4];                                     // this wave's own tiles (ib = cw)
+      {
+        auto tile = [&](int ib, int jb, bool own_q) -> bf16x4 {
+          floatx4 acc = zero4();
+#pragma unroll
+          for (int kb = 0; kb < DK / 32; ++kb) {
+            const bf16* kp = s.ks + kj_rd + 16 * jb * KP + 32 * kb;
+            const bf16* qp = s.qs + kj_rd + 16 * ib * KP + 32 * kb;
+            const bf16x8 kr = cat8(*reinterpret_cast<const bf16x4*>(kp), *reinterpret_cast<const bf16x4*>(kp + 16));
+            const bf16x8 qr = own_q ? qf[kb] : cat8(*reinterpret_cast<const bf16x4*>(qp), *reinterpret_cast<const bf16x4*>(qp + 16));
+            acc = mfma_bf16(kr, qr, acc);
+          }
+          bf16x4 out;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) out[ii] = (bf16)((jb < ib || c >= 4 * g + ii) ? acc[ii] : 0.f);
+          return out;
+        };
+        const bf16x4 z4 = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f};
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) ptl[jb] = z4;
+        if (cw == 0) {
+          ptl[0] = tile(0, 0, true);
+          *reinterpret_cast<bf16x4*>(PX + (0 * 64 + lane) * 4) = tile(2, 0, false);
+          *reinterpret_cast<bf16x4*>(PX + (1 * 64 + lane) * 4) = tile(3, 0, false);
+        } else if (cw == 1) {
+          ptl[0] = tile(1, 0, true);
+          ptl[1] = tile(1, 1, true);
+          *reinterpret_cast<bf16x4*>(PX + (2 * 64 + lane) * 4) = tile(3, 1, false);
+        } else if (cw == 2) {
+          ptl[1] = tile(2, 1, true);
+          ptl[2] = tile(2, 2, true);
+        } else {
+          ptl[2] = tile(3, 2, true);
+          ptl[3] = tile(3, 3, true);
+        }
       }
       lds_barrier();                                     // B1
       // ---- phase 2: o^T = v_new^T P^T + (QE S~)^T -> HBM; S~ update -> SB ----
@@ -305,8 +345,13 @@ void kda_scan_split_kernel(KdaScanArgs a) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           if (kb == 0 || cw >= 2) {
-            const bf16* pp = s.ps + p_rd + 32 * kb;
-            const bf16x8 pb = cat8(*reinterpret_cast<const bf16x4*>(pp), *reinterpret_cast<const bf16x4*>(pp + 16));
+            bf16x4 lo = ptl[2 * kb], hi = ptl[2 * kb + 1];
+            if (kb == 0 && cw == 2) lo = *reinterpret_cast<const bf16x4*>(PX + (0 * 64 + lane) * 4);
+            if (kb == 0 && cw == 3) {
+              lo = *reinterpret_cast<const bf16x4*>(PX + (1 * 64 + lane) * 4);
+              hi = *reinterpret_cast<const bf16x4*>(PX + (2 * 64 + lane) * 4);
+            }
+            const bf16x8 pb = cat8(lo, hi);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
               OT[nt] = mfma_bf16(*reinterpret_cast<const bf16x8*>(VX + (kb * NT + nt) * FRAG + frag), pb, OT[nt]);
@@ -332,15 +377,8 @@ void kda_scan_split_kernel(KdaScanArgs a) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sb), ro, ra + 8 * DV * 4, 0,
                                                kCachePolicyNT);
       }
-      // S~ <- e^{G_last} (.) S~ + KR^T v_new  (the decay scales the state rows = key channels)
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const floatx4 d4 = *reinterpret_cast<const floatx4*>(s.dec + 32 * cw + 16 * r + 4 * g);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) S[r][nt][ii] *= d4[ii];
-      }
+      // S~ <- e^{G_last} (.) (S~ + KB^T v_new)  (the decay scales the state rows = key channels;
+      // e^{G_last} KB^T is the (k e^{G_last - G})^T of the recurrence)
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const bf16* k0 = s.ks + kt_rd + 16 * r;
@@ -351,6 +389,14 @@ void kda_scan_split_kernel(KdaScanArgs a) {
           for (int nt = 0; nt < NT; ++nt)
             S[r][nt] = mfma_bf16(at, *reinterpret_cast<const bf16x8*>(VX + (kb * NT + nt) * FRAG + frag), S[r][nt]);
         }
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const floatx4 d4 = *reinterpret_cast<const floatx4*>(s.dec + 32 * cw + 16 * r + 4 * g);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) S[r][nt][ii] *= d4[ii];
       }
       publish();
       lds_barrier();                                     // B2

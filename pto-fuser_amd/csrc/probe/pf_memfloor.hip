@@ -15,7 +15,7 @@
 //
 // A second form replays the kernels' own address pattern: the chunk images read from tensors laid
 // out as the kernels read them (k, q, v and o as [B*H, T, 128], T as [B*H, NC, 64, 64]; KDA's
-// W, QE, KR as [B*H, NC, 64, 128], P and T diag(beta) as [B*H, NC, 64, 64], v as [B*H, T, 128],
+// W, QE, KB as [B*H, NC, 64, 128], T diag(beta) as [B*H, NC, 64, 64], v as [B*H, T, 128],
 // the decay as [B*H, NC, 128] fp32), with the kernels' chain-to-workgroup mapping (the slices of
 // a chain on one XCD) and each loader lane's 16-byte vectors, so the floor includes what the
 // tensors' strides (powers of two at these shapes) cost the memory system.
@@ -30,7 +30,7 @@ namespace {
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSteps = 96;        // chunks streamed per launch
 constexpr int kGroups = 256;      // one workgroup per CU
-constexpr int kMaxKiB = 72;       // largest chunk image (LDS: two stages)
+constexpr int kMaxKiB = 64;       // largest chunk image (LDS: two stages)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
@@ -123,19 +123,19 @@ constexpr int executed_steps(int steps = kSteps) {
 
 // Tensors of one workload in the kernels' layout.
 struct Tensors {
-  const unsigned char* a[7];   // GDN: k, q, T, v; KDA: W, QE, KR, P, v, decay, T diag(beta)
+  const unsigned char* a[6];   // GDN: k, q, T, v; KDA: W, QE, KB, v, decay, T diag(beta)
   unsigned char* o;            // [chains, T, 128] fp32
 };
 
 // The kernels' traffic at their own addresses.  KDA false: GDN stage 2 (per loader wave and
-// chunk 4 k, 4 q, 2 T vectors of 1 KiB and one v load per lane); KDA true: 4 W, 4 QE, 4 KR, 2 P,
+// chunk 4 k, 4 q, 2 T vectors of 1 KiB and one v load per lane); KDA true: 4 W, 4 QE, 4 KB,
 // 2 T diag(beta), one v and one decay load per lane.  NCOL: columns per slice (32 or 16), NC: chunks per chain,
 // STEPS: chunks streamed, NTST: o stores non-temporal, LD / ST: issue the loads / the stores.
 template <bool KDA, int NCOL, int NC, int STEPS, bool NTST, bool LD, bool ST>
 __global__ __launch_bounds__(256) void layout_kernel(Tensors t, uint32_t* sink, int chains) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[2][kMaxKiB * 1024];
   constexpr int NS = 128 / NCOL;                    // slices per chain
-  constexpr int NV = KDA ? 18 : 11;                 // 16-byte loads per lane and chunk
+  constexpr int NV = KDA ? 16 : 11;                 // 16-byte loads per lane and chunk
   constexpr uint32_t Tlen = NC * 64;
   const int lane = threadIdx.x & 63, lt = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -155,11 +155,10 @@ __global__ __launch_bounds__(256) void layout_kernel(Tensors t, uint32_t* sink, 
   const __amdgpu_buffer_rsrc_t r0 = rsrc(t.a[0] + (size_t)bh * row_bytes, row_bytes);
   const __amdgpu_buffer_rsrc_t r1 = rsrc(t.a[1] + (size_t)bh * row_bytes, row_bytes);
   const __amdgpu_buffer_rsrc_t r2 = rsrc(t.a[2] + (size_t)bh * (KDA ? row_bytes : NC * 8192u), KDA ? row_bytes : NC * 8192u);
-  const __amdgpu_buffer_rsrc_t r3 = rsrc(t.a[3] + (size_t)bh * (KDA ? NC * 8192u : row_bytes), KDA ? NC * 8192u : row_bytes);
-  const __amdgpu_buffer_rsrc_t r4 = rsrc(t.a[KDA ? 4 : 3] + (size_t)bh * row_bytes, row_bytes);
-  const __amdgpu_buffer_rsrc_t r5 = rsrc(t.a[KDA ? 5 : 3] + (size_t)bh * (KDA ? NC * 512u : row_bytes), KDA ? NC * 512u : row_bytes);
+  const __amdgpu_buffer_rsrc_t r3 = rsrc(t.a[3] + (size_t)bh * row_bytes, row_bytes);
+  const __amdgpu_buffer_rsrc_t r4 = rsrc(t.a[KDA ? 4 : 3] + (size_t)bh * (KDA ? NC * 512u : row_bytes), KDA ? NC * 512u : row_bytes);
+  const __amdgpu_buffer_rsrc_t r5 = rsrc(t.a[KDA ? 5 : 3] + (size_t)bh * (KDA ? NC * 8192u : row_bytes), KDA ? NC * 8192u : row_bytes);
   const __amdgpu_buffer_rsrc_t ro = rsrc(t.o + (size_t)bh * Tlen * 512u, Tlen * 512u);
-  const __amdgpu_buffer_rsrc_t r6 = rsrc(t.a[6] + (size_t)bh * NC * 8192u, NC * 8192u);
   // a slice's rows of a [T, 128] bf16 tile (v or U): NCOL * 2 bytes per row, 64 rows; lanes past
   // the tile's vectors repeat (as the kernels' loaders do)
   constexpr int VPR = NCOL / 8, VV = 64 * VPR;
@@ -179,16 +178,14 @@ __global__ __launch_bounds__(256) void layout_kernel(Tensors t, uint32_t* sink, 
       if constexpr (!KDA) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) s.v[8 + k] = __builtin_amdgcn_raw_buffer_load_b128(r2, lo, c8 + 4096u * k, 0);
-        s.v[10] = __builtin_amdgcn_raw_buffer_load_b128(r4, tile_off, (uint32_t)ch * 64u * 256u, 0);
+        s.v[10] = __builtin_amdgcn_raw_buffer_load_b128(r3, tile_off, (uint32_t)ch * 64u * 256u, 0);
       } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k) s.v[8 + k] = __builtin_amdgcn_raw_buffer_load_b128(r2, lo, c16 + 4096u * k, 0);
+        s.v[12] = __builtin_amdgcn_raw_buffer_load_b128(r3, tile_off, (uint32_t)ch * 64u * 256u, 0);
+        s.v[13] = __builtin_amdgcn_raw_buffer_load_b128(r4, 16u * (lt & 31), (uint32_t)ch * 512u, 0);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) s.v[12 + k] = __builtin_amdgcn_raw_buffer_load_b128(r3, lo, c8 + 4096u * k, 0);
-        s.v[14] = __builtin_amdgcn_raw_buffer_load_b128(r4, tile_off, (uint32_t)ch * 64u * 256u, 0);
-        s.v[15] = __builtin_amdgcn_raw_buffer_load_b128(r5, 16u * (lt & 31), (uint32_t)ch * 512u, 0);
-#pragma unroll
-        for (int k = 0; k < 2; ++k) s.v[16 + k] = __builtin_amdgcn_raw_buffer_load_b128(r6, lo, c8 + 4096u * k, 0);
+        for (int k = 0; k < 2; ++k) s.v[14 + k] = __builtin_amdgcn_raw_buffer_load_b128(r5, lo, c8 + 4096u * k, 0);
       }
     }
   };
@@ -333,24 +330,24 @@ int main() {
   // GDN config 4 (B1 H32 T32768): 16-column slices, k 16 + q 16 + T 8 KiB + the v tile (2 KiB,
   // loaded as 4 KiB: one 16-byte load per loader lane), o 16 x 4 B per token through the cache.
   if (!pattern<44, 8, 4096, false>(b, "gdn_config4", 512)) return 1;
-  // KDA config 5 (B2 H32 T8192): 32-column slices, W, QE, KR 16 KiB each + P 8 + T diag(beta) 8
+  // KDA config 5 (B2 H32 T8192): 32-column slices, W, QE, KB 16 KiB each + T diag(beta) 8
   // + v 4 KiB + the decay (one 16-byte load per loader lane: 4 KiB), o streamed past the cache.
-  if (!pattern<72, 4, 8192, true>(b, "kda_config5", 128)) return 1;
+  if (!pattern<64, 4, 8192, true>(b, "kda_config5", 128)) return 1;
 
   // The same three in the kernels' tensor layout (one allocation per tensor, sized for the
   // largest workload: 32 chains x 32768 tokens).
   const size_t rows = (size_t)32 * 32768 * 256;           // [B*H, T, 128] bf16, 256 MiB
-  unsigned char* ten[8] = {};
-  const size_t sizes[8] = {rows, rows, rows, rows, rows, (size_t)64 * 128 * 512, rows, rows * 2};
-  for (int i = 0; i < 8; ++i)
+  unsigned char* ten[7] = {};
+  const size_t sizes[7] = {rows, rows, rows, rows, (size_t)64 * 128 * 512, rows, rows * 2};
+  for (int i = 0; i < 7; ++i)
     if (!ok(hipMalloc(&ten[i], sizes[i]), "hipMalloc") || !ok(hipMemset(ten[i], 1, sizes[i]), "hipMemset")) return 1;
-  const Tensors t{{ten[0], ten[1], ten[2], ten[3], ten[4], ten[5], ten[6]}, ten[7]};
+  const Tensors t{{ten[0], ten[1], ten[2], ten[3], ten[4], ten[5]}, ten[6]};
   if (!layout_pattern<false, 32, 64, 64, true>(b, t, 64, "gdn_headline")) return 1;
   if (!layout_pattern<false, 16, 512, 96, false>(b, t, 32, "gdn_config4")) return 1;
   // config 4's pattern with the o stores non-temporal (the kernel stores them through L2)
   if (!layout_pattern<false, 16, 512, 96, true>(b, t, 32, "gdn_c4_nt")) return 1;
   if (!layout_pattern<true, 32, 128, 96, true>(b, t, 64, "kda_config5")) return 1;
-  for (int i = 0; i < 8; ++i) (void)hipFree(ten[i]);
+  for (int i = 0; i < 7; ++i) (void)hipFree(ten[i]);
   (void)hipFree(b.src);
   (void)hipFree(b.dst);
   (void)hipFree(b.sink);

@@ -92,12 +92,13 @@ def test_fp32_workspace_holds_bf16(lib, B, H, T, C):
 
 
 def test_kda_workspace_and_rejects(lib):
-    # W, U, QE, KR (bf16 [M,C,128] each) + P (bf16 [M,C,C]) + DEC (fp32 [M,128]), 256-B aligned
+    # W, QE, k e^-G (bf16 [M,C,128] each) + T diag(beta) (bf16 [M,C,C]) + DEC (fp32 [M,128]),
+    # 256-B aligned
     M = 2 * 32 * 128
-    want = 4 * ((M * 64 * 128 * 2 + 255) // 256 * 256) + (M * 64 * 64 * 2 + 255) // 256 * 256 \
+    want = 3 * ((M * 64 * 128 * 2 + 255) // 256 * 256) + (M * 64 * 64 * 2 + 255) // 256 * 256 \
         + (M * 128 * 4 + 255) // 256 * 256
     assert lib.pf_kda_workspace_bytes(2, 32, 8192, 64, 128, 128, _hip.PF_DTYPE_BF16) == want
-    # fp32 operands: the same images in fp32
+    # fp32 operands: W, U, QE, KR, P and DEC in fp32
     M1 = 128
     want32 = 4 * ((M1 * 64 * 128 * 4 + 255) // 256 * 256) + (M1 * 64 * 64 * 4 + 255) // 256 * 256 \
         + (M1 * 128 * 4 + 255) // 256 * 256

@@ -99,11 +99,11 @@ def test_cpu_baseline_child_reports_cores():
 def test_kda_model():
     m = bench.kda_model(2, 32, 8192, C, DK, DV)
     assert m["units"] == 2 * 32 * 128
-    # stage 1: q, k, g, beta in; W, QE, KR, T diag(beta), the 12 P blocks, the decay out
-    s1 = 2 * C * DK * 2 + C * DK * 4 + C * 4 + 3 * C * DK * 2 + C * C * 2 + 12 * 256 * 2 + DK * 4
-    # stage 2: W, QE, KR, T diag(beta), P (whole), v, the decay in; o out
-    s2 = 3 * C * DK * 2 + 2 * C * C * 2 + C * DV * 2 + DK * 4 + C * DV * 4
-    assert m["bytes_per_unit"] == s1 + s2 == 244992
+    # stage 1: q, k, g, beta in; W, QE, KB, T diag(beta), the decay out
+    s1 = 2 * C * DK * 2 + C * DK * 4 + C * 4 + 3 * C * DK * 2 + C * C * 2 + DK * 4
+    # stage 2: W, QE, KB, T diag(beta), v, the decay in; o out (the causal score stays on the chip)
+    s2 = 3 * C * DK * 2 + C * C * 2 + C * DV * 2 + DK * 4 + C * DV * 4
+    assert m["bytes_per_unit"] == s1 + s2 == 230656
     # compulsory: q, k, v, g, beta in and o out, plus the final state
     assert m["compulsory_bytes"] == m["units"] * (3 * C * DK * 2 + C * DK * 4 + C * 4 + C * DV * 4) \
         + 2 * 32 * DK * DV * 4
