@@ -67,6 +67,18 @@ def test_kda_bf16_strong_decay():
     _check("KDA bf16 B1 H2 T512 strong decay", o, h, o_ref, h_ref)
 
 
+def test_kda_bf16_extreme_decay():
+    """g up to ~ -4 per token: a channel's within-chunk cumulative log decay reaches -65, so
+    e^-G of the key operand reaches ~1e28 and e^G of the query operand ~1e-28 (both still inside
+    the fp32 / bf16 exponent range, as in the reference's fp32 factors), with h0."""
+    announce("KDA bf16 B1 H2 T256 extreme decay h0")
+    inp = make_delta_inputs(1, 2, 256, kind="kda", dtype=torch.bfloat16, seed=13, gate_scale=1.0,
+                            h0_std=0.02)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    _check("KDA bf16 B1 H2 T256 extreme decay h0", o, h, o_ref, h_ref)
+
+
 def test_kda_bf16_config5():
     announce("KDA bf16 B2 H32 T8192")
     inp = make_delta_inputs(2, 32, 8192, kind="kda", dtype=torch.bfloat16, seed=5)
