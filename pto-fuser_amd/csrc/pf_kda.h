@@ -96,7 +96,8 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
   // LDS regions, by phase:
   //   [0, 3 TILE) bf16 : tiles a | b | (spare)   (the fp32 g staging [C][DK] aliases the start)
   //   [3 TILE, ..) fp32: A [C][CP]
-  // after the products of A: T (fp32) takes the third tile, T diag(beta) (bf16) takes A.
+  // after the products of A: T (fp32) takes the third tile, T diag(beta) (bf16) takes A, and W
+  // passes through the b tile on its way to HBM.
   static_assert(C * CP * 4 <= TILE * 2 && C * DK * 4 <= 3 * TILE * 2 && C * TPB * 2 <= C * CP * 4, "LDS aliasing");
   __shared__ __attribute__((aligned(16))) bf16 tiles[3 * TILE];
   __shared__ __attribute__((aligned(16))) float As[C * CP];
@@ -215,19 +216,20 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
            (j0 + 2 <= i) ? t4[2] * b4[2] : 0.f, (j0 + 3 <= i) ? t4[3] * b4[3] : 0.f);
   }
   lds_barrier();
-  // TB to HBM for stage 2: thread tid writes row tid / 4, columns 16 (tid % 4) .. +15
-  {
-    const int i = tid >> 2, j0 = 16 * (tid & 3);
-    bf16* dst = a.TB + ((size_t)m * C + i) * C + j0;
-    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(Tb + i * TPB + j0);
-    *reinterpret_cast<uint4*>(dst + 8) = *reinterpret_cast<const uint4*>(Tb + i * TPB + j0 + 8);
+  // TB to HBM for stage 2: vector u = tid + 256 h (h = 0, 1) is row u / 8, columns 8 (u % 8) ..,
+  // so each store instruction writes eight whole 128-byte rows
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int u = tid + 256 * h, i = u >> 3, j0 = 8 * (u & 7);
+    *reinterpret_cast<uint4*>(a.TB + ((size_t)m * C + i) * C + j0) =
+        *reinterpret_cast<const uint4*>(Tb + i * TPB + j0);
   }
 
   // ---- 7. W^T = a^T (T diag beta)^T ---------------------------------------------------------
   // Wave w owns the 16-row blocks mb = 2w, 2w+1 of the dk dimension.  A operand: a^T by
   // transpose reads (lane (c,g) gets rows j = 32kb + 4g + 0..3 and +16 of column 16mb + c);
   // B operand: rows i = 16nb + c of T diag(beta) at the same (permuted) j.  The D registers hold
-  // W[i][16mb + 4g .. +3]: four consecutive columns, one 8-byte store.
+  // W[i][16mb + 4g .. +3]: four consecutive columns.
   {
     floatx4 accW[2][4];
 #pragma unroll
@@ -249,14 +251,19 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
         }
       }
     }
+    // staged in the b tile (free since A was formed), then written as whole rows: a store
+    // instruction of four scattered 32-byte pieces per row was measured 7 % slower for the kernel
 #pragma unroll
     for (int mb2 = 0; mb2 < 2; ++mb2)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const size_t e = ((size_t)m * C + 16 * nb + c) * DK + 16 * (2 * w + mb2) + 4 * g;
-        const floatx4 x = accW[mb2][nb];
-        store4(a.W + e, x[0], x[1], x[2], x[3]);
-      }
+      for (int nb = 0; nb < 4; ++nb)
+        store4(bt + (16 * nb + c) * KP + 16 * (2 * w + mb2) + 4 * g, accW[mb2][nb][0], accW[mb2][nb][1],
+               accW[mb2][nb][2], accW[mb2][nb][3]);
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<uint4*>(a.W + (row0 + rb + 16 * i) * DK + vc) =
+          *reinterpret_cast<const uint4*>(bt + (rb + 16 * i) * KP + vc);
   }
 }
 

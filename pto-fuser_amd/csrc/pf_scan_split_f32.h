@@ -8,9 +8,10 @@
 //
 //   1.  partial Y_w = k[:, rows of w] S_w and (q S)_w for all 64 tokens     -> LDS
 //   2a. wave w: Y = sum of the partials and r = beta v - beta e^G Y for token tiles 0..w, and
-//       v_new of token tile w = sum_jb T[w][jb] r_jb (T is lower triangular)   -> LDS
-//   2b. every wave reads all of v_new; wave w: o of token tile 3 - w = scale e^G (sum of the
-//       q S partials) + P v_new -> HBM (o tiles 3..0 balance the v_new tiles 0..3: 20 products
+//       v_new of token tile w = sum_jb T[w][jb] r_jb (T is lower triangular)   -> LDS; the sum
+//       of the q S partials of token tile 3 - w
+//   2b. every wave reads all of v_new; wave w: o of token tile 3 - w = scale e^G (q S) +
+//       P v_new -> HBM (o tiles 3..0 balance the v_new tiles 0..3: 20 products
 //       per wave); S_w <- e^{G_last} S_w + k[:, rows of w]^T (e^{G_last - G} v_new)
 //
 // so every wave carries 64 + 20 + 32 products per chunk instead of one wave's ~460 (forming all
@@ -19,7 +20,8 @@
 // computed and written into LDS where its last reader is done: each wave's own slice of k and q
 // (the only columns it reads) after its own last read, T, P and the gate tables (two buffers:
 // T and P as their ten lower 16x16 tiles) after the barrier that ends step 1, v after the one
-// that ends step 2a.  Three barriers per chunk, and no copy section between them.
+// that ends step 2a.  Two barriers per chunk, and no copy section between them: every exchange
+// tile is last read before the second, so the next chunk's first step may overwrite them.
 #pragma once
 
 #include "pf_scan_args.h"
@@ -175,7 +177,12 @@ void scan_split_f32_kernel(ScanOutArgs a) {
     load_tpg(nx2);
     const float* ts = tsb[cb];
     const float* ps = psb[cb];
-    // ---- 2a. wave w: r for token tiles 0..w, v_new tile w = sum_jb T[w][jb] r_jb -> VX ----
+    // ---- 2a. wave w: r for token tiles 0..w, v_new tile w = sum_jb T[w][jb] r_jb -> VX; the
+    //      (q S) partials of its o tile 3 - w summed here, so no exchange is read after B2 ----
+    const int ot = 3 - w;                              // o tiles 3..0 balance v_new tiles 0..3
+    floatx4 O = QP[ot * 64 + lane];
+#pragma unroll
+    for (int w2 = 1; w2 < 4; ++w2) O += QP[(w2 * 4 + ot) * 64 + lane];
     {
       floatx4 V = zero4();
 #pragma unroll
@@ -205,10 +212,6 @@ void scan_split_f32_kernel(ScanOutArgs a) {
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) VN[ib] = VX[ib * 64 + lane];
     {
-      const int ot = 3 - w;                            // o tiles 3..0 balance v_new tiles 0..3
-      floatx4 O = QP[ot * 64 + lane];
-#pragma unroll
-      for (int w2 = 1; w2 < 4; ++w2) O += QP[(w2 * 4 + ot) * 64 + lane];
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[cb][16 * ot + 4 * g + ii];
 #pragma unroll
@@ -240,7 +243,9 @@ void scan_split_f32_kernel(ScanOutArgs a) {
     }
     store_k();                                         // this wave's k slice is read
     load_k(nx2);
-    lds_barrier();                                     // B3: the chunk's exchanges are read
+    // no third barrier: the next chunk's step 1 writes YP (last read in 2a) and QP (last read
+    // in 2a), its 2a writes VX after B1 (every wave then is past this 2b), and T, P and the gate
+    // tables alternate between two buffers
   }
   if (a.h_final) {
 #pragma unroll
