@@ -11,7 +11,9 @@
 //
 // Stage 1 (kda_local_kernel, one workgroup per chunk) does what needs the whole chunk's gates at
 // once: the cumsum, the gated operands, A and the inverse; it writes W, TB = T diag(beta),
-// QE = scale q e^G, KB = b (bf16) and the chunk decay e^{G_last} (fp32).  Stage 2
+// QE = scale q e^G, KB = b (bf16) and the chunk decay e^{G_last} (fp32), W, TB, QE and KB as
+// whole 128-byte lines stored non-temporally (they are far larger than the caches and read only
+// by stage 2: stored through the caches they cost stage 2 4 % of its time).  Stage 2
 // (kda_scan_split_kernel, pf_kda_scan.h, one workgroup per (chain, 32-column slice)) carries S in
 // registers through the chain:
 //
@@ -181,8 +183,8 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
       qv[e] = (bf16)(a.scale * (float)qx[e] * eg);
     }
     const size_t e0 = (row0 + r) * DK + vc;
-    *reinterpret_cast<bf16x8*>(a.QE + e0) = qv;
-    *reinterpret_cast<bf16x8*>(a.KB + e0) = bv;
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, qv), reinterpret_cast<u32x4*>(a.QE + e0));
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, bv), reinterpret_cast<u32x4*>(a.KB + e0));
     // swizzled row tiles: two 4-element groups per vector
     const int o0 = kda_swz<KP>(r, vc), o1 = kda_swz<KP>(r, vc + 4);
     *reinterpret_cast<bf16x4*>(at + o0) = bf16x4{av[0], av[1], av[2], av[3]};
@@ -221,8 +223,8 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int u = tid + 256 * h, i = u >> 3, j0 = 8 * (u & 7);
-    *reinterpret_cast<uint4*>(a.TB + ((size_t)m * C + i) * C + j0) =
-        *reinterpret_cast<const uint4*>(Tb + i * TPB + j0);
+    __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(Tb + i * TPB + j0),
+                                reinterpret_cast<u32x4*>(a.TB + ((size_t)m * C + i) * C + j0));
   }
 
   // ---- 7. W^T = a^T (T diag beta)^T ---------------------------------------------------------
@@ -262,8 +264,8 @@ __global__ __launch_bounds__(256) void kda_local_kernel(KdaLocalArgs a) {
     lds_barrier();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4*>(a.W + (row0 + rb + 16 * i) * DK + vc) =
-          *reinterpret_cast<const uint4*>(bt + (rb + 16 * i) * KP + vc);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(bt + (rb + 16 * i) * KP + vc),
+                                  reinterpret_cast<u32x4*>(a.W + (row0 + rb + 16 * i) * DK + vc));
   }
 }
 
