@@ -204,6 +204,19 @@ def test_deltanet_bf16_fused(B, H, T):
            bf16=True)
 
 
+def test_deltanet_bf16_longest_chain():
+    """No decay at the longest chain the forward takes in one call at this size (T = 32768,
+    512 chunks) with h0: the state's bf16 rounding never washes out, so this is where its error
+    builds up most; it levels off near 1e-2 on h (|h| up to ~3)."""
+    announce("DeltaNet bf16 fused B1 H2 T32768 h0")
+    inp = make_delta_inputs(1, 2, 32768, kind="deltanet", dtype=torch.bfloat16, seed=3, h0_std=0.02)
+    o, h = _run(inp)
+    x = as_oracle_inputs(inp)
+    ref = deltanet_reference(x["q"], x["k"], x["v"], x["beta"], C=64, h0=x["h0"], dtype=np.float64)
+    _check("DeltaNet bf16 fused B1 H2 T32768 h0", o, h, ref["o"].reshape(o.shape), ref["final"],
+           bf16=True)
+
+
 def test_gdn_bf16_config2():
     announce("GDN bf16 B4 H16 T4096")
     inp = make_delta_inputs(4, 16, 4096, kind="gdn", dtype=torch.bfloat16, seed=0)
