@@ -114,9 +114,10 @@ int pf_gdn_scan_output_exec(const void* q, const void* k, const void* v, const f
  * examples/attention/_kda_full.py (host gate prep :78-103, the gated kkt / per-dim flash
  * templates template.py:335-397 and the per-dim chunk_h_scan of transforms/kda.py:20-85 with
  * scan_fused.h:143-180), the per-channel gate being applied on the device: stage 1 forms the
- * gated operands k e^G, k e^-G, q e^G, k e^{G_last - G} from g, inverts (I + A) and builds the WY
- * factor W, T diag(beta) (bf16 operands; U with fp32 operands) and the score; stage 2 forms U from
- * T diag(beta) and v (bf16 operands) and carries the state in registers with a per-channel decay.
+ * gated operands k e^G, k e^-G and q e^G from g, inverts (I + A) and builds the WY factor W and
+ * T diag(beta) (fp32 operands: also k e^{G_last - G}, U and the causal score); with bf16 operands
+ * stage 2 forms U = T diag(beta) v and the causal score from the tiles it stages, and it carries
+ * the state in registers with a per-channel decay.
  * Math: kda_reference (_kda_full.py:42-76) plus an initial state h0 and the final state.
  *   q, k [B,H,T,DK] and v [B,H,T,DV] of `dtype`; beta [B,H,T] fp32; g [B,H,T,DK] fp32
  *   (per-token, per-channel log decay, summed within each chunk of C tokens by the kernel);
