@@ -184,7 +184,7 @@ void scan_split_f32_kernel(ScanOutArgs a) {
 #pragma unroll
     for (int w2 = 1; w2 < 4; ++w2) O += QP[(w2 * 4 + ot) * 64 + lane];
     {
-      floatx4 V = zero4();
+      floatx4 V = zero4(), V2 = zero4();                 // two accumulators: shorter chains
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         if (jb <= w) {
@@ -199,10 +199,13 @@ void scan_split_f32_kernel(ScanOutArgs a) {
           }
           const floatx4 ta = *reinterpret_cast<const floatx4*>(ts + score_tile_index(w, jb) * TT + c * TR + 4 * g);
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) V = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[ii], R[ii], V, 0, 0, 0);
+          for (int ii = 0; ii < 4; ++ii) {
+            if (ii & 1) V2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[ii], R[ii], V2, 0, 0, 0);
+            else V = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[ii], R[ii], V, 0, 0, 0);
+          }
         }
       }
-      VX[w * 64 + lane] = V;
+      VX[w * 64 + lane] = V + V2;
     }
     lds_barrier();                                     // B2: v_new written, v read
     store_v();
@@ -214,14 +217,19 @@ void scan_split_f32_kernel(ScanOutArgs a) {
     {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) O[ii] *= EG[cb][16 * ot + 4 * g + ii];
+      floatx4 O2 = zero4();
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         if (jb <= ot) {
           const floatx4 pa = *reinterpret_cast<const floatx4*>(ps + score_tile_index(ot, jb) * TT + c * TR + 4 * g);
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) O = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ii], VN[jb][ii], O, 0, 0, 0);
+          for (int ii = 0; ii < 4; ++ii) {
+            if (ii & 1) O2 = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ii], VN[jb][ii], O2, 0, 0, 0);
+            else O = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ii], VN[jb][ii], O, 0, 0, 0);
+          }
         }
       }
+      O += O2;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
         __builtin_nontemporal_store(O[ii], a.o + ((size_t)bh * Tlen + (size_t)ch * C + 16 * ot + 4 * g + ii) * DV + col0 + c);
@@ -230,15 +238,18 @@ void scan_split_f32_kernel(ScanOutArgs a) {
       const float dl = DL[cb][0];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        floatx4 acc = S[r] * dl;
+        floatx4 acc = S[r] * dl, acc2 = zero4();        // two accumulators: shorter chains
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
             const int t = 16 * jb + 4 * g + ii;
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[t * KP + 32 * w + 16 * r + c], EL[cb][t] * VN[jb][ii], acc, 0, 0, 0);
+            if (ii & 1)
+              acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[t * KP + 32 * w + 16 * r + c], EL[cb][t] * VN[jb][ii], acc2, 0, 0, 0);
+            else
+              acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[t * KP + 32 * w + 16 * r + c], EL[cb][t] * VN[jb][ii], acc, 0, 0, 0);
           }
-        S[r] = acc;
+        S[r] = acc + acc2;
       }
     }
     store_k();                                         // this wave's k slice is read
