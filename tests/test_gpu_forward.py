@@ -190,6 +190,18 @@ def test_gdn_bf16_wide_slices_unaligned_chains(B, H, T):
     _check(f"GDN bf16 B{B} H{H} T{T} h0 (32-col)", o, h, o_ref, h_ref, bf16=True)
 
 
+@pytest.mark.parametrize("B,H,T", [(16, 32, 128), (7, 73, 192)])
+def test_gdn_bf16_many_chains(B, H, T):
+    """512 and 511 chains: eight and about eight scan workgroups per CU over the run (several
+    generations of workgroups), with the XCD-aware chain mapping (B*H % 8 == 0) and without."""
+    announce(f"GDN bf16 B{B} H{H} T{T} h0 (many chains)")
+    inp = make_delta_inputs(B, H, T, kind="gdn", dtype=torch.bfloat16, seed=B * 70 + H,
+                            h0_std=0.02)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    _check(f"GDN bf16 B{B} H{H} T{T} h0 (many chains)", o, h, o_ref, h_ref, bf16=True)
+
+
 @pytest.mark.parametrize("B,H,T", [(4, 16, 1024), (1, 2, 256)])
 def test_deltanet_bf16_fused(B, H, T):
     """DeltaNet (g = None) through the fused bf16 forward, against deltanet_reference

@@ -67,6 +67,18 @@ def test_kda_bf16_strong_decay():
     _check("KDA bf16 B1 H2 T512 strong decay", o, h, o_ref, h_ref)
 
 
+@pytest.mark.parametrize("B,H,T", [(8, 64, 128), (7, 37, 64)])
+def test_kda_bf16_many_chains(B, H, T):
+    """512 and 259 chains (several generations of scan workgroups), with the XCD-aware chain
+    mapping (B*H % 8 == 0) and without, with h0."""
+    announce(f"KDA bf16 B{B} H{H} T{T} h0 (many chains)")
+    inp = make_delta_inputs(B, H, T, kind="kda", dtype=torch.bfloat16, seed=B * 30 + H,
+                            h0_std=0.02)
+    o, h = _run(inp)
+    o_ref, h_ref = _oracle(inp)
+    _check(f"KDA bf16 B{B} H{H} T{T} h0 (many chains)", o, h, o_ref, h_ref)
+
+
 def test_kda_bf16_extreme_decay():
     """g up to ~ -4 per token: a channel's within-chunk cumulative log decay reaches -65, so
     e^-G of the key operand reaches ~1e28 and e^G of the query operand ~1e-28 (both still inside
